@@ -1,0 +1,221 @@
+/*
+ * mlxcat_hip.h -- C ABI of the MI355X (gfx950) n-gram speculative-decode step.
+ *
+ * This is the drop-in boundary a Swift C target (`CMLXCatHIP`) binds in place
+ * of the Metal path behind mlxcat's ContinuousBatchGenerator.  Every entry
+ * point names the reference interface it replaces (local-ai-cat/mlxcat, paths
+ * relative to its root; MLX / mlx-swift-lm symbols are external SwiftPM
+ * dependencies pinned at Package.swift:61-95).
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a negative MC_E_* code on
+ *     failure; mc_last_error() returns a thread-local message.  In Swift these
+ *     map to `throws` (BatchGeneratorError / BatchKVCacheError) and at the
+ *     scheduler to Response(token: -1, finishReason: .failed(msg))
+ *     (Sources/MLXCat/TrackB/Scheduler.swift:532-541).
+ *   - Host buffers are caller-owned; device memory is owned by the handles.
+ *   - Handles are not thread-safe.  Each batch handle owns one HIP stream, which
+ *     matches the reference's actor serialisation (Scheduler.swift:13).
+ *   - Tokens are int32, logits bf16 stored as uint16.
+ *   - Weights use MLX's 4-bit affine format with group size 64: wq[N][K/8]
+ *     uint32 with element j of a word at bits 4j, scales/biases [N][K/64] bf16
+ *     (group cost 64*bits/8 + 4 bytes: Sources/MLXCat/TrackB/KVQuantizationPolicy.swift:12-14).
+ *     The library repacks them once, losslessly, into its MFMA tile layout.
+ */
+#ifndef MLXCAT_HIP_H
+#define MLXCAT_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define MC_OK 0
+#define MC_E_INVALID (-1)  /* bad argument or shape */
+#define MC_E_HIP (-2)      /* HIP runtime error */
+#define MC_E_NOMEM (-3)    /* device allocation failed */
+#define MC_E_STATE (-4)    /* call not valid in the handle's current state */
+#define MC_E_CAPACITY (-5) /* row, context or history capacity exceeded */
+
+/* ---- architectures ---- */
+#define MC_ARCH_QWEN3 0
+#define MC_ARCH_LLAMA 1
+#define MC_ARCH_QWEN3_MOE 2
+/* The reference's scheduler test doubles, SchedulerSpeculativeDecodingTests.swift:174-261:
+ * logits +20 at next(token) and -20 elsewhere, next(1)=2, next(2)=3, else 1;
+ * the mismatching variant maps 3 -> 4. */
+#define MC_ARCH_FAKE_REPEATING 100
+#define MC_ARCH_FAKE_MISMATCHING 101
+
+/* linear tensor slots (mc_model_set_linear / mc_model_get_linear) */
+#define MC_W_Q 0
+#define MC_W_K 1
+#define MC_W_V 2
+#define MC_W_O 3
+#define MC_W_GATE 4
+#define MC_W_UP 5
+#define MC_W_DOWN 6
+#define MC_W_ROUTER 11
+#define MC_W_EMBED 100   /* layer ignored; tied models use it as the LM head */
+#define MC_W_LM_HEAD 101 /* untied models only */
+/* norm slots (mc_model_set_norm) */
+#define MC_N_INPUT 7
+#define MC_N_POST 8
+#define MC_N_Q 9
+#define MC_N_K 10
+#define MC_N_FINAL 102
+
+/* acceptance rules */
+#define MC_ACCEPT_ALL_OR_NOTHING 0 /* the reference rule, BatchGenerator.swift:906-947 */
+#define MC_ACCEPT_PREFIX 1         /* longest agreeing prefix + correction, per-row rollback */
+
+typedef struct mc_model mc_model;
+typedef struct mc_batch mc_batch;
+
+/* Model shape.  Mirrors the config.json keys an MLX checkpoint carries
+ * (Sources/MLXCatNative/NativeModelEngine.swift:1147-1231). */
+typedef struct mc_model_config {
+  int32_t arch;
+  int32_t n_layers, hidden, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;
+  int32_t tied_embeddings;
+  float rms_eps, rope_theta;
+  int32_t n_experts, n_experts_per_tok, moe_intermediate;
+} mc_model_config;
+
+/* SpeculativeDecodingConfiguration, Sources/MLXCat/TrackB/BatchGenerator.swift:10-29.
+ * Clamped like the Swift initialiser: K >= 0, max_suffix >= 1, min_context >= 2. */
+typedef struct mc_spec_config {
+  int32_t enabled;
+  int32_t max_proposal_tokens; /* K */
+  int32_t max_suffix_tokens;   /* default 16 */
+  int32_t min_context_tokens;  /* default 8 */
+  int32_t acceptance;          /* MC_ACCEPT_* for greedy rows */
+  int32_t single_row_only;     /* reference gate rowUIDs.count == 1 (BatchGenerator.swift:959) */
+  int32_t greedy_only;         /* reference gate temperature == 0 && no RNG (:963,970) */
+} mc_spec_config;
+
+/* Subset of SamplingParameters (Sources/MLXCat/TrackB/Sampling.swift:139-217) used by the step. */
+typedef struct mc_sampling {
+  float temperature;   /* 0 = greedy argmax, lowest index on ties */
+  float top_p;         /* applied when 0 < top_p < 1, Sampling.swift:847-858 */
+  int32_t has_seed;
+  uint64_t seed;       /* per-request RNG (BatchGenerator.swift:1089-1091) */
+  int32_t n_eos;
+  int32_t eos[8];
+  int32_t reject_token; /* tool-call trigger (BatchGenerator.swift:920-923); -1 = none */
+} mc_sampling;
+
+/* SpeculativeDecodingStats, BatchGenerator.swift:31-38 */
+typedef struct mc_spec_stats {
+  int64_t proposed, accepted, proposal_batches, rejected_batches;
+} mc_spec_stats;
+
+/* ---- errors / device ---- */
+const char* mc_last_error(void);
+/* Selects the HIP device for subsequent handle creation. */
+int mc_set_device(int device);
+
+/* ---- model: replaces the mlx-swift-lm LanguageModel (Qwen3 / Llama / Qwen3-MoE modules),
+ * protocol shape at Tests/MLXCatTests/SchedulerSpeculativeDecodingTests.swift:174-223 ---- */
+int mc_model_create(const mc_model_config* cfg, mc_model** out);
+void mc_model_destroy(mc_model* m);
+/* Fill every tensor with the seeded synthetic generator (random-init workloads). */
+int mc_model_init_synthetic(mc_model* m, uint64_t seed);
+/* Load one quantized linear from host MLX tensors (a .weight/.scales/.biases triplet);
+ * expert >= 0 selects a MoE expert's gate/up/down. */
+int mc_model_set_linear(mc_model* m, int32_t layer, int32_t which, int32_t expert,
+                        const uint32_t* wq, const uint16_t* scales, const uint16_t* biases);
+/* Export a linear back to MLX format (host buffers of the MLX shapes). */
+int mc_model_get_linear(mc_model* m, int32_t layer, int32_t which, int32_t expert, uint32_t* wq,
+                        uint16_t* scales, uint16_t* biases);
+int mc_model_set_norm(mc_model* m, int32_t layer, int32_t which, const uint16_t* w);
+
+/* ---- batch state: replaces BatchKVCache (Sources/MLXCat/TrackB/BatchCache.swift:37-433),
+ * the per-row token histories and currentTokens of ContinuousBatchGenerator
+ * (BatchGenerator.swift:144-215).  Per-row contiguous bf16 K/V with a length; fork,
+ * commit and rollback are O(1) length updates instead of copy() (BatchCache.swift:426-433)
+ * plus trim (:403-424). ---- */
+int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, int32_t max_draft,
+                    const mc_spec_config* spec, mc_batch** out);
+void mc_batch_destroy(mc_batch* b);
+/* ContinuousBatchGenerator.insert after admission (BatchGenerator.swift:344-474,
+ * Scheduler.swift:599-668): prefill the prompt into `row`, sample the first token,
+ * seed the speculative history with prompt + first token.  *finished = 1 (EOS) or
+ * 2 (length) when the request ends at admission. */
+int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt,
+                    int32_t max_tokens, const mc_sampling* sp, int32_t* first_token,
+                    int32_t* finished);
+/* Admit a row whose first n_ctx-1 positions of K/V were filled by
+ * mc_batch_fill_synthetic_kv; the last token of ctx is the pending current token. */
+int mc_batch_insert_prefilled(mc_batch* b, int32_t row, const int32_t* ctx, int32_t n_ctx,
+                              int32_t max_tokens, const mc_sampling* sp);
+/* Seeded synthetic bf16 K/V for positions [0, n) of a row (stress workloads). */
+int mc_batch_fill_synthetic_kv(mc_batch* b, int32_t row, int32_t n, uint64_t seed);
+/* ContinuousBatchGenerator.remove (BatchGenerator.swift:476-480). */
+int mc_batch_remove(mc_batch* b, int32_t row);
+/* BatchKVCache.trim (BatchCache.swift:403-424): drop min(n, len) trailing positions of
+ * every active row; returns the trimmed count (>= 0) or an error. */
+int mc_batch_trim(mc_batch* b, int32_t n);
+/* Per-row ragged rollback (no reference counterpart: the reference drops the forked
+ * cache wholesale).  Drops min(n, len) trailing positions of one row. */
+int mc_batch_rollback(mc_batch* b, int32_t row, int32_t n);
+int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len);
+/* Copy one row's K (which_v = 0) or V (1) of one layer to host: [n_kv][len][d] bf16. */
+int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t which_v, uint16_t* out);
+int mc_batch_history(mc_batch* b, int32_t row, int32_t* out, int32_t cap, int32_t* len);
+
+/* ---- forward: LanguageModel.callAsFunction(LMInput.Text, cache:, state:)
+ * (BatchGenerator.swift:900-904).  counts[r] new tokens for each listed row, positions
+ * kv_len[row] + j; K/V appended and kv_len advanced.  logits_host [sum counts][vocab]
+ * bf16 (NULL to skip). ---- */
+int mc_forward(mc_batch* b, int32_t nrows, const int32_t* rows, const int32_t* counts,
+               const int32_t* tokens, uint16_t* logits_host);
+
+/* ---- n-gram proposer: ContinuousBatchGenerator.proposeSuffixTokens
+ * (BatchGenerator.swift:982-1010), run on the GPU over host-supplied histories.
+ * hist_off[B+1] are offsets into hist; limit[B] per row; out[B][max(limit)] and
+ * out_len[B] (0 = nil). ---- */
+int mc_ngram_propose(const int32_t* hist, const int64_t* hist_off, int32_t B,
+                     int32_t max_suffix, int32_t min_context, const int32_t* limit,
+                     int32_t out_stride, int32_t* out, int32_t* out_len);
+
+/* ---- acceptance: the loop over TokenSampler.sample at BatchGenerator.swift:906-935,
+ * run on the GPU over host logits.  Per row r: logits rows [row_off[r], row_off[r] +
+ * n_draft[r] + 1), drafts[r][0..n_draft[r]).  Greedy rows use `acceptance`; rows with
+ * temperature > 0 use speculative sampling with 32-bit uniforms derived from
+ * (seed, counter[r]).  Outputs: n_emit[r] tokens in out_tokens[r][0 .. draft_stride],
+ * (row stride draft_stride + 1), kv_keep[r] positions of the verified block to keep,
+ * n_accepted[r] drafts accepted. ---- */
+int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* row_off,
+              const int32_t* drafts, int32_t draft_stride, const int32_t* n_draft,
+              const mc_sampling* sp, const uint64_t* counter, int32_t acceptance,
+              int32_t* out_tokens, int32_t* n_emit, int32_t* kv_keep, int32_t* n_accepted);
+
+/* ---- fused step: ContinuousBatchGenerator.next() -> speculativeNext()
+ * (BatchGenerator.swift:593-600, 875-955) plus Scheduler.step's finish handling
+ * (Scheduler.swift:361-427), for every active row at once: propose, verify forward,
+ * accept, roll back, append history; one host synchronisation.  out_tokens[row][K+1],
+ * out_counts[row] tokens emitted, out_finish[row] 0 running / 1 stop (EOS) / 2 length;
+ * finished rows are removed.  forced_accept (NULL = none) caps each row's accepted drafts
+ * (stress workloads with a forced accept-length schedule). ---- */
+int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_tokens, int32_t* out_counts,
+            int32_t* out_finish);
+/* SpeculativeDecodingStats accumulated by mc_step (Scheduler.swift:474-476). */
+int mc_batch_stats(mc_batch* b, mc_spec_stats* out);
+/* Widths of the warm-cache forwards issued so far (the reference tests' decode-call
+ * accounting, SchedulerSpeculativeDecodingTests.swift:202-208); returns the count. */
+int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap);
+
+/* ---- timing support ---- */
+/* Average device time (ms) of each kernel class over the last mc_step when profiling is
+ * enabled; used by bench.py for the live roofline.  kind: 0 = dequant GEMV (all),
+ * 1 = attention, 2 = whole verify step. */
+int mc_batch_set_profiling(mc_batch* b, int32_t enabled);
+int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

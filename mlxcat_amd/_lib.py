@@ -1,0 +1,340 @@
+"""ctypes binding of libmlxcat_hip.so (the C ABI in include/mlxcat_hip.h).
+
+The HIP library is the only compute path: if it is missing this module raises,
+there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libmlxcat_hip.so")
+
+ARCH_QWEN3, ARCH_LLAMA, ARCH_QWEN3_MOE = 0, 1, 2
+ARCH_FAKE_REPEATING, ARCH_FAKE_MISMATCHING = 100, 101
+W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN, W_ROUTER = 0, 1, 2, 3, 4, 5, 6, 11
+W_EMBED, W_LM_HEAD = 100, 101
+N_INPUT, N_POST, N_Q, N_K, N_FINAL = 7, 8, 9, 10, 102
+ACCEPT_ALL_OR_NOTHING, ACCEPT_PREFIX = 0, 1
+
+# every symbol the header declares (checked by the CPU tests)
+EXPORTS = [
+    "mc_last_error", "mc_set_device", "mc_model_create", "mc_model_destroy", "mc_model_init_synthetic",
+    "mc_model_set_linear", "mc_model_get_linear", "mc_model_set_norm", "mc_batch_create", "mc_batch_destroy",
+    "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
+    "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_history",
+    "mc_forward", "mc_ngram_propose", "mc_accept", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
+    "mc_batch_set_profiling", "mc_batch_profile",
+]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [
+        ("arch", C.c_int32), ("n_layers", C.c_int32), ("hidden", C.c_int32), ("n_q_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("intermediate", C.c_int32), ("vocab", C.c_int32),
+        ("tied_embeddings", C.c_int32), ("rms_eps", C.c_float), ("rope_theta", C.c_float),
+        ("n_experts", C.c_int32), ("n_experts_per_tok", C.c_int32), ("moe_intermediate", C.c_int32),
+    ]
+
+
+class SpecConfig(C.Structure):
+    _fields_ = [
+        ("enabled", C.c_int32), ("max_proposal_tokens", C.c_int32), ("max_suffix_tokens", C.c_int32),
+        ("min_context_tokens", C.c_int32), ("acceptance", C.c_int32), ("single_row_only", C.c_int32),
+        ("greedy_only", C.c_int32),
+    ]
+
+
+class Sampling(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float), ("top_p", C.c_float), ("has_seed", C.c_int32), ("seed", C.c_uint64),
+        ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("reject_token", C.c_int32),
+    ]
+
+
+class SpecStats(C.Structure):
+    _fields_ = [("proposed", C.c_int64), ("accepted", C.c_int64), ("proposal_batches", C.c_int64),
+                ("rejected_batches", C.c_int64)]
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Loads the library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -m mlxcat_amd.build` "
+                          "(there is no CPU fallback)")
+    L = C.CDLL(path)
+    P, I32, U64 = C.c_void_p, C.c_int32, C.c_uint64
+    sig = {
+        "mc_last_error": (C.c_char_p, []),
+        "mc_set_device": (C.c_int, [C.c_int]),
+        "mc_model_create": (C.c_int, [P, P]),
+        "mc_model_destroy": (None, [P]),
+        "mc_model_init_synthetic": (C.c_int, [P, U64]),
+        "mc_model_set_linear": (C.c_int, [P, I32, I32, I32, P, P, P]),
+        "mc_model_get_linear": (C.c_int, [P, I32, I32, I32, P, P, P]),
+        "mc_model_set_norm": (C.c_int, [P, I32, I32, P]),
+        "mc_batch_create": (C.c_int, [P, I32, I32, I32, P, P]),
+        "mc_batch_destroy": (None, [P]),
+        "mc_batch_insert": (C.c_int, [P, I32, P, I32, I32, P, P, P]),
+        "mc_batch_insert_prefilled": (C.c_int, [P, I32, P, I32, I32, P]),
+        "mc_batch_fill_synthetic_kv": (C.c_int, [P, I32, I32, U64]),
+        "mc_batch_remove": (C.c_int, [P, I32]),
+        "mc_batch_trim": (C.c_int, [P, I32]),
+        "mc_batch_rollback": (C.c_int, [P, I32, I32]),
+        "mc_batch_kv_len": (C.c_int, [P, I32, P]),
+        "mc_batch_read_kv": (C.c_int, [P, I32, I32, I32, P]),
+        "mc_batch_history": (C.c_int, [P, I32, P, I32, P]),
+        "mc_forward": (C.c_int, [P, I32, P, P, P, P]),
+        "mc_ngram_propose": (C.c_int, [P, P, I32, I32, I32, P, I32, P, P]),
+        "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, I32, P, P, P, P]),
+        "mc_step": (C.c_int, [P, P, P, P, P]),
+        "mc_batch_stats": (C.c_int, [P, P]),
+        "mc_batch_call_widths": (C.c_int, [P, P, I32]),
+        "mc_batch_set_profiling": (C.c_int, [P, I32]),
+        "mc_batch_profile": (C.c_int, [P, I32, P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        raise HipError(rc, load().mc_last_error().decode(errors="replace"))
+    return rc
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _i32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1) -> Sampling:
+    sp = Sampling()
+    sp.temperature = float(temperature)
+    sp.top_p = float(top_p)
+    sp.has_seed = 0 if seed is None else 1
+    sp.seed = 0 if seed is None else int(seed)
+    if len(eos) > 8:
+        raise ValueError("at most 8 EOS ids")
+    sp.n_eos = len(eos)
+    for i, e in enumerate(eos):
+        sp.eos[i] = int(e)
+    sp.reject_token = int(reject_token)
+    return sp
+
+
+class Model:
+    """Device-resident 4-bit decoder (the LanguageModel the verify forward runs)."""
+
+    def __init__(self, cfg: dict):
+        L = load()
+        self.cfg = ModelConfig(**cfg)
+        h = C.c_void_p()
+        _check(L.mc_model_create(C.byref(self.cfg), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().mc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def init_synthetic(self, seed: int) -> None:
+        _check(load().mc_model_init_synthetic(self.h, seed))
+
+    def _lshape(self, which: int):
+        c = self.cfg
+        H, d, nq, nkv, I = c.hidden, c.head_dim, c.n_q_heads, c.n_kv_heads, c.intermediate
+        return {W_Q: (nq * d, H), W_K: (nkv * d, H), W_V: (nkv * d, H), W_O: (H, nq * d), W_GATE: (I, H),
+                W_UP: (I, H), W_DOWN: (H, I), W_EMBED: (c.vocab, H), W_LM_HEAD: (c.vocab, H)}[which]
+
+    def set_linear(self, layer: int, which: int, wq, scales, biases, expert: int = -1) -> None:
+        N, K = self._lshape(which)
+        wq = np.ascontiguousarray(wq, dtype=np.uint32).reshape(N, K // 8)
+        s = np.ascontiguousarray(scales, dtype=np.uint16).reshape(N, K // 64)
+        b = np.ascontiguousarray(biases, dtype=np.uint16).reshape(N, K // 64)
+        _check(load().mc_model_set_linear(self.h, layer, which, expert, _p(wq), _p(s), _p(b)))
+
+    def get_linear(self, layer: int, which: int, expert: int = -1):
+        N, K = self._lshape(which)
+        wq = np.zeros((N, K // 8), dtype=np.uint32)
+        s = np.zeros((N, K // 64), dtype=np.uint16)
+        b = np.zeros((N, K // 64), dtype=np.uint16)
+        _check(load().mc_model_get_linear(self.h, layer, which, expert, _p(wq), _p(s), _p(b)))
+        return wq, s, b
+
+    def set_norm(self, layer: int, which: int, w) -> None:
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        _check(load().mc_model_set_norm(self.h, layer, which, _p(w)))
+
+
+class Batch:
+    """Device state of a continuous batch: per-row KV, token histories, sampling."""
+
+    def __init__(self, model: Model, max_rows: int, max_ctx: int, spec: dict, max_draft: int | None = None):
+        L = load()
+        self.model = model
+        self.spec = SpecConfig(**spec)
+        self.R = max_rows
+        self.K = self.spec.max_proposal_tokens if self.spec.enabled else 0
+        self.K1 = self.K + 1
+        h = C.c_void_p()
+        _check(L.mc_batch_create(model.h, max_rows, max_ctx, self.K if max_draft is None else max_draft,
+                                 C.byref(self.spec), C.byref(h)))
+        self.h = h
+        self._tok = np.zeros((self.R, self.K1), dtype=np.int32)
+        self._cnt = np.zeros(self.R, dtype=np.int32)
+        self._fin = np.zeros(self.R, dtype=np.int32)
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().mc_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def insert(self, row: int, prompt, max_tokens: int, sampling: Sampling):
+        p = _i32(prompt)
+        tok, fin = C.c_int32(), C.c_int32()
+        _check(load().mc_batch_insert(self.h, row, _p(p), len(p), max_tokens, C.byref(sampling), C.byref(tok),
+                                      C.byref(fin)))
+        return tok.value, fin.value
+
+    def fill_synthetic_kv(self, row: int, n: int, seed: int) -> None:
+        _check(load().mc_batch_fill_synthetic_kv(self.h, row, n, seed))
+
+    def insert_prefilled(self, row: int, ctx, max_tokens: int, sampling: Sampling) -> None:
+        c = _i32(ctx)
+        _check(load().mc_batch_insert_prefilled(self.h, row, _p(c), len(c), max_tokens, C.byref(sampling)))
+
+    def remove(self, row: int) -> None:
+        _check(load().mc_batch_remove(self.h, row))
+
+    def trim(self, n: int) -> int:
+        return _check(load().mc_batch_trim(self.h, n))
+
+    def rollback(self, row: int, n: int) -> None:
+        _check(load().mc_batch_rollback(self.h, row, n))
+
+    def kv_len(self, row: int) -> int:
+        v = C.c_int32()
+        _check(load().mc_batch_kv_len(self.h, row, C.byref(v)))
+        return v.value
+
+    def read_kv(self, layer: int, row: int, which_v: int) -> np.ndarray:
+        c = self.model.cfg
+        out = np.zeros((c.n_kv_heads, self.kv_len(row), c.head_dim), dtype=np.uint16)
+        _check(load().mc_batch_read_kv(self.h, layer, row, which_v, _p(out)))
+        return out
+
+    def history(self, row: int) -> list[int]:
+        n = C.c_int32()
+        _check(load().mc_batch_history(self.h, row, None, 0, C.byref(n)))
+        out = np.zeros(max(n.value, 1), dtype=np.int32)
+        _check(load().mc_batch_history(self.h, row, _p(out), n.value, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def forward(self, rows, counts, tokens, want_logits: bool = True):
+        rows, counts, tokens = _i32(rows), _i32(counts), _i32(tokens)
+        M = int(counts.sum())
+        lg = np.zeros((M, self.model.cfg.vocab), dtype=np.uint16) if want_logits else None
+        _check(load().mc_forward(self.h, len(rows), _p(rows), _p(counts), _p(tokens), _p(lg)))
+        return lg
+
+    def step(self, forced_accept=None):
+        fa = _i32(forced_accept) if forced_accept is not None else None
+        _check(load().mc_step(self.h, _p(fa), _p(self._tok), _p(self._cnt), _p(self._fin)))
+        return self._tok.copy(), self._cnt.copy(), self._fin.copy()
+
+    def stats(self) -> dict:
+        s = SpecStats()
+        _check(load().mc_batch_stats(self.h, C.byref(s)))
+        return {"proposed": s.proposed, "accepted": s.accepted, "proposal_batches": s.proposal_batches,
+                "rejected_batches": s.rejected_batches}
+
+    def call_widths(self) -> list[int]:
+        n = _check(load().mc_batch_call_widths(self.h, None, 0))
+        out = np.zeros(max(n, 1), dtype=np.int32)
+        load().mc_batch_call_widths(self.h, _p(out), n)
+        return out[:n].tolist()
+
+    def set_profiling(self, enabled: bool) -> None:
+        _check(load().mc_batch_set_profiling(self.h, 1 if enabled else 0))
+
+    def profile(self, kind: int):
+        ms, by, n = C.c_double(), C.c_double(), C.c_int32()
+        _check(load().mc_batch_profile(self.h, kind, C.byref(ms), C.byref(by), C.byref(n)))
+        return ms.value, by.value, n.value
+
+
+def ngram_propose(histories, max_suffix: int, min_context: int, limits) -> list[list[int]]:
+    """GPU n-gram proposer over host histories (one proposal per history)."""
+    B = len(histories)
+    off = np.zeros(B + 1, dtype=np.int64)
+    for i, h in enumerate(histories):
+        off[i + 1] = off[i] + len(h)
+    flat = _i32(np.concatenate([np.asarray(h, dtype=np.int32) for h in histories]) if B else np.zeros(0))
+    lim = _i32(limits)
+    stride = max(1, int(lim.max()) if B else 1)
+    out = np.zeros((B, stride), dtype=np.int32)
+    n = np.zeros(B, dtype=np.int32)
+    _check(load().mc_ngram_propose(_p(flat) if flat.size else None, _p(off), B, max_suffix, min_context, _p(lim),
+                                   stride, _p(out), _p(n)))
+    return [out[i, : n[i]].tolist() for i in range(B)]
+
+
+def accept(logits_rows: list[np.ndarray], drafts: list[list[int]], samplings: list[Sampling], counters,
+           acceptance: int):
+    """GPU acceptance over host logits: row r has len(drafts[r]) + 1 logits rows."""
+    B = len(drafts)
+    V = logits_rows[0].shape[1]
+    stride = max(1, max(len(d) for d in drafts))
+    off = np.zeros(B + 1, dtype=np.int64)
+    for r in range(B):
+        off[r + 1] = off[r] + len(drafts[r]) + 1
+    lg = np.ascontiguousarray(np.concatenate(logits_rows, axis=0), dtype=np.uint16)
+    dr = np.zeros((B, stride), dtype=np.int32)
+    nd = np.zeros(B, dtype=np.int32)
+    for r, d in enumerate(drafts):
+        dr[r, : len(d)] = d
+        nd[r] = len(d)
+    sp = (Sampling * B)(*samplings)
+    ctr = np.ascontiguousarray(counters, dtype=np.uint64)
+    out = np.zeros((B, stride + 1), dtype=np.int32)
+    n_emit = np.zeros(B, dtype=np.int32)
+    keep = np.zeros(B, dtype=np.int32)
+    nacc = np.zeros(B, dtype=np.int32)
+    _check(load().mc_accept(_p(lg), V, B, _p(off), _p(dr), stride, _p(nd), C.cast(sp, C.c_void_p), _p(ctr),
+                            acceptance, _p(out), _p(n_emit), _p(keep), _p(nacc)))
+    return [out[r, : n_emit[r]].tolist() for r in range(B)], keep.tolist(), nacc.tolist()

@@ -1,0 +1,1127 @@
+// mc_api.hip -- the C ABI (include/mlxcat_hip.h): model and batch handles, the verify
+// forward, the fused speculative step captured as one HIP graph per batch, and the
+// standalone proposer / acceptance entry points.  Host code only; the kernels live in
+// mc_gemv.hip, mc_kernels.hip and mc_step.hip.
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mc_gemv.hpp"
+#include "mc_kernels.hpp"
+#include "mc_step.hpp"
+
+namespace mc {
+
+static thread_local std::string g_err;
+void set_error(const std::string& msg) { g_err = msg; }
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+int hip_fail(hipError_t e, const char* what, const char* file, int line) {
+  char buf[512];
+  snprintf(buf, sizeof buf, "HIP error '%s' in %s (%s:%d)", hipGetErrorString(e), what, file, line);
+  g_err = buf;
+  return e == hipErrorOutOfMemory ? MC_E_NOMEM : MC_E_HIP;
+}
+
+static int g_device = 0;
+constexpr int PREFILL_CHUNK = 64;
+
+template <typename T>
+static int dev_alloc(T** p, size_t n) {
+  *p = nullptr;
+  if (n == 0) n = 1;
+  hipError_t e = hipMalloc((void**)p, n * sizeof(T));
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc", __FILE__, __LINE__);
+  return MC_OK;
+}
+template <typename T>
+static int dev_zero(T** p, size_t n) {
+  int rc = dev_alloc(p, n);
+  if (rc) return rc;
+  MC_HIP(hipMemset(*p, 0, (n ? n : 1) * sizeof(T)));
+  return MC_OK;
+}
+
+static int qlinear_alloc(QLinear* L, int N, int K) {
+  if (N <= 0 || K <= 0 || K % 64) return fail(MC_E_INVALID, "linear: K must be a positive multiple of 64");
+  L->N = N;
+  L->K = K;
+  L->NT = (N + 15) / 16;
+  L->GP = (K + 127) / 128;
+  int rc = dev_zero(&L->qw, L->qw_words());
+  if (rc) return rc;
+  return dev_zero(&L->sb, L->sb_words());
+}
+static void qlinear_free(QLinear* L) {
+  if (L->qw) (void)hipFree(L->qw);
+  if (L->sb) (void)hipFree(L->sb);
+  L->qw = nullptr;
+  L->sb = nullptr;
+}
+
+}  // namespace mc
+
+using namespace mc;
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+struct mc_model {
+  mc_model_config cfg{};
+  int device = 0;
+  bool fake = false;
+  struct Layer {
+    QLinear qkv, o, gateup, down;
+    uint16_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  };
+  std::vector<Layer> layers;
+  QLinear embed, lm_head;
+  uint16_t* final_norm = nullptr;
+  hipStream_t st = nullptr;
+  const QLinear& head() const { return cfg.tied_embeddings ? embed : lm_head; }
+};
+
+extern "C" const char* mc_last_error(void) { return g_err.c_str(); }
+
+extern "C" int mc_set_device(int device) {
+  int n = 0;
+  MC_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(MC_E_INVALID, "mc_set_device: no such device");
+  g_device = device;
+  MC_HIP(hipSetDevice(device));
+  return MC_OK;
+}
+
+static int norm_ones(uint16_t** p, int n) {
+  int rc = dev_alloc(p, (size_t)n);
+  if (rc) return rc;
+  std::vector<uint16_t> h((size_t)n, (uint16_t)0x3F80);
+  MC_HIP(hipMemcpy(*p, h.data(), (size_t)n * 2, hipMemcpyHostToDevice));
+  return MC_OK;
+}
+
+extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
+  if (!cfg || !out) return fail(MC_E_INVALID, "mc_model_create: null argument");
+  *out = nullptr;
+  MC_HIP(hipSetDevice(g_device));
+  auto* m = new mc_model();
+  m->cfg = *cfg;
+  m->device = g_device;
+  const auto& c = *cfg;
+  if (c.arch == MC_ARCH_FAKE_REPEATING || c.arch == MC_ARCH_FAKE_MISMATCHING) {
+    if (c.vocab < 8) { delete m; return fail(MC_E_INVALID, "fake model needs vocab >= 8"); }
+    m->fake = true;
+    *out = m;
+    return MC_OK;
+  }
+  if (c.arch != MC_ARCH_QWEN3 && c.arch != MC_ARCH_LLAMA) {
+    delete m;
+    return fail(MC_E_INVALID, "mc_model_create: architecture not supported by this build");
+  }
+  if (c.n_layers <= 0 || c.hidden % 64 || c.head_dim > 128 || c.head_dim % 2 || c.n_kv_heads <= 0 ||
+      c.n_q_heads % c.n_kv_heads || c.intermediate % 64 || c.vocab <= 0 || (c.n_q_heads * c.head_dim) % 64) {
+    delete m;
+    return fail(MC_E_INVALID, "mc_model_create: unsupported shape");
+  }
+  int rc = MC_OK;
+  MC_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
+  const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
+  m->layers.resize((size_t)c.n_layers);
+  for (auto& L : m->layers) {
+    if ((rc = qlinear_alloc(&L.qkv, (nq + 2 * nkv) * d, H))) break;
+    if ((rc = qlinear_alloc(&L.o, H, nq * d))) break;
+    if ((rc = qlinear_alloc(&L.gateup, 2 * I, H))) break;
+    if ((rc = qlinear_alloc(&L.down, H, I))) break;
+    if ((rc = norm_ones(&L.in_norm, H)) || (rc = norm_ones(&L.post_norm, H))) break;
+    if (c.arch == MC_ARCH_QWEN3) {
+      if ((rc = norm_ones(&L.q_norm, d)) || (rc = norm_ones(&L.k_norm, d))) break;
+    }
+  }
+  if (!rc) rc = qlinear_alloc(&m->embed, c.vocab, H);
+  if (!rc && !c.tied_embeddings) rc = qlinear_alloc(&m->lm_head, c.vocab, H);
+  if (!rc) rc = norm_ones(&m->final_norm, H);
+  if (!rc) rc = gemv_setup_lds();
+  if (rc) {
+    mc_model_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return MC_OK;
+}
+
+extern "C" void mc_model_destroy(mc_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  for (auto& L : m->layers) {
+    qlinear_free(&L.qkv);
+    qlinear_free(&L.o);
+    qlinear_free(&L.gateup);
+    qlinear_free(&L.down);
+    for (uint16_t* p : {L.in_norm, L.post_norm, L.q_norm, L.k_norm})
+      if (p) (void)hipFree(p);
+  }
+  qlinear_free(&m->embed);
+  qlinear_free(&m->lm_head);
+  if (m->final_norm) (void)hipFree(m->final_norm);
+  if (m->st) (void)hipStreamDestroy(m->st);
+  delete m;
+}
+
+// Where an MLX tensor lands inside the fused tile tensors: (linear, row offset, row stride, rows).
+static int linear_slot(mc_model* m, int layer, int which, QLinear** L, int* off, int* stride, int* rows, int* K) {
+  const auto& c = m->cfg;
+  const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
+  if (which == MC_W_EMBED) { *L = &m->embed; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK; }
+  if (which == MC_W_LM_HEAD) {
+    if (c.tied_embeddings) return fail(MC_E_INVALID, "tied model has no separate lm_head");
+    *L = &m->lm_head; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK;
+  }
+  if (layer < 0 || layer >= c.n_layers) return fail(MC_E_INVALID, "layer out of range");
+  auto& Ly = m->layers[(size_t)layer];
+  switch (which) {
+    case MC_W_Q: *L = &Ly.qkv; *off = 0; *stride = 1; *rows = nq * d; *K = H; return MC_OK;
+    case MC_W_K: *L = &Ly.qkv; *off = nq * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
+    case MC_W_V: *L = &Ly.qkv; *off = (nq + nkv) * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
+    case MC_W_O: *L = &Ly.o; *off = 0; *stride = 1; *rows = H; *K = nq * d; return MC_OK;
+    case MC_W_GATE: *L = &Ly.gateup; *off = 0; *stride = 2; *rows = I; *K = H; return MC_OK;
+    case MC_W_UP: *L = &Ly.gateup; *off = 1; *stride = 2; *rows = I; *K = H; return MC_OK;
+    case MC_W_DOWN: *L = &Ly.down; *off = 0; *stride = 1; *rows = H; *K = I; return MC_OK;
+    default: return fail(MC_E_INVALID, "unknown linear slot");
+  }
+}
+
+extern "C" int mc_model_set_linear(mc_model* m, int32_t layer, int32_t which, int32_t expert, const uint32_t* wq,
+                                   const uint16_t* scales, const uint16_t* biases) {
+  if (!m || !wq || !scales || !biases) return fail(MC_E_INVALID, "mc_model_set_linear: null argument");
+  if (m->fake) return fail(MC_E_STATE, "fake model has no weights");
+  if (expert >= 0) return fail(MC_E_INVALID, "MoE experts are not supported by this build");
+  MC_HIP(hipSetDevice(m->device));
+  QLinear* L;
+  int off, stride, rows, K;
+  int rc = linear_slot(m, layer, which, &L, &off, &stride, &rows, &K);
+  if (rc) return rc;
+  uint32_t* dq;
+  uint16_t *ds, *db;
+  const size_t nw = (size_t)rows * (K / 8), ns = (size_t)rows * (K / 64);
+  if ((rc = dev_alloc(&dq, nw))) return rc;
+  if ((rc = dev_alloc(&ds, ns))) { (void)hipFree(dq); return rc; }
+  if ((rc = dev_alloc(&db, ns))) { (void)hipFree(dq); (void)hipFree(ds); return rc; }
+  hipError_t e = hipMemcpy(dq, wq, nw * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(ds, scales, ns * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(db, biases, ns * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    rc = qlinear_repack(*L, off, stride, rows, dq, ds, db, m->st);
+    if (!rc) e = hipStreamSynchronize(m->st);
+  }
+  (void)hipFree(dq);
+  (void)hipFree(ds);
+  (void)hipFree(db);
+  if (e != hipSuccess) return hip_fail(e, "mc_model_set_linear", __FILE__, __LINE__);
+  return rc;
+}
+
+extern "C" int mc_model_get_linear(mc_model* m, int32_t layer, int32_t which, int32_t expert, uint32_t* wq,
+                                   uint16_t* scales, uint16_t* biases) {
+  if (!m || !wq || !scales || !biases) return fail(MC_E_INVALID, "mc_model_get_linear: null argument");
+  if (m->fake) return fail(MC_E_STATE, "fake model has no weights");
+  if (expert >= 0) return fail(MC_E_INVALID, "MoE experts are not supported by this build");
+  MC_HIP(hipSetDevice(m->device));
+  QLinear* L;
+  int off, stride, rows, K;
+  int rc = linear_slot(m, layer, which, &L, &off, &stride, &rows, &K);
+  if (rc) return rc;
+  uint32_t* dq;
+  uint16_t *ds, *db;
+  const size_t nw = (size_t)rows * (K / 8), ns = (size_t)rows * (K / 64);
+  if ((rc = dev_alloc(&dq, nw))) return rc;
+  if ((rc = dev_alloc(&ds, ns))) { (void)hipFree(dq); return rc; }
+  if ((rc = dev_alloc(&db, ns))) { (void)hipFree(dq); (void)hipFree(ds); return rc; }
+  rc = qlinear_export(*L, off, stride, rows, dq, ds, db, m->st);
+  hipError_t e = hipSuccess;
+  if (!rc) e = hipStreamSynchronize(m->st);
+  if (!rc && e == hipSuccess) e = hipMemcpy(wq, dq, nw * 4, hipMemcpyDeviceToHost);
+  if (!rc && e == hipSuccess) e = hipMemcpy(scales, ds, ns * 2, hipMemcpyDeviceToHost);
+  if (!rc && e == hipSuccess) e = hipMemcpy(biases, db, ns * 2, hipMemcpyDeviceToHost);
+  (void)hipFree(dq);
+  (void)hipFree(ds);
+  (void)hipFree(db);
+  if (e != hipSuccess) return hip_fail(e, "mc_model_get_linear", __FILE__, __LINE__);
+  return rc;
+}
+
+extern "C" int mc_model_set_norm(mc_model* m, int32_t layer, int32_t which, const uint16_t* w) {
+  if (!m || !w) return fail(MC_E_INVALID, "mc_model_set_norm: null argument");
+  if (m->fake) return fail(MC_E_STATE, "fake model has no weights");
+  MC_HIP(hipSetDevice(m->device));
+  const auto& c = m->cfg;
+  uint16_t* dst = nullptr;
+  int n = 0;
+  if (which == MC_N_FINAL) {
+    dst = m->final_norm;
+    n = c.hidden;
+  } else {
+    if (layer < 0 || layer >= c.n_layers) return fail(MC_E_INVALID, "layer out of range");
+    auto& L = m->layers[(size_t)layer];
+    switch (which) {
+      case MC_N_INPUT: dst = L.in_norm; n = c.hidden; break;
+      case MC_N_POST: dst = L.post_norm; n = c.hidden; break;
+      case MC_N_Q: dst = L.q_norm; n = c.head_dim; break;
+      case MC_N_K: dst = L.k_norm; n = c.head_dim; break;
+      default: return fail(MC_E_INVALID, "unknown norm slot");
+    }
+    if (!dst) return fail(MC_E_INVALID, "this architecture has no such norm");
+  }
+  MC_HIP(hipMemcpy(dst, w, (size_t)n * 2, hipMemcpyHostToDevice));
+  return MC_OK;
+}
+
+// synthetic norm weights: bf16 1 + (h % 32 - 16) / 128 (matches the oracle)
+static std::vector<uint16_t> synth_norm(uint64_t seed, uint64_t tid, int n) {
+  std::vector<uint16_t> w((size_t)n);
+  const uint64_t base = mix64(seed ^ mix64(tid ^ 0x4E4F524Dull));
+  for (int i = 0; i < n; ++i) {
+    const uint64_t h = mix64(base ^ (uint64_t)i);
+    const int k = (int)(h % 32u) - 16;
+    w[(size_t)i] = f32_to_bf16(1.0f + (float)k / 128.0f);
+  }
+  return w;
+}
+
+extern "C" int mc_model_init_synthetic(mc_model* m, uint64_t seed) {
+  if (!m) return fail(MC_E_INVALID, "mc_model_init_synthetic: null model");
+  if (m->fake) return MC_OK;
+  MC_HIP(hipSetDevice(m->device));
+  const auto& c = m->cfg;
+  const int d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate, H = c.hidden;
+  int rc;
+  for (int l = 0; l < c.n_layers; ++l) {
+    auto& L = m->layers[(size_t)l];
+    if ((rc = qlinear_synth(L.qkv, 0, 1, nq * d, synth_base(seed, tensor_id(l, T_Q)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.qkv, nq * d, 1, nkv * d, synth_base(seed, tensor_id(l, T_K)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.qkv, (nq + nkv) * d, 1, nkv * d, synth_base(seed, tensor_id(l, T_V)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.o, 0, 1, H, synth_base(seed, tensor_id(l, T_O)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.gateup, 0, 2, I, synth_base(seed, tensor_id(l, T_GATE)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.gateup, 1, 2, I, synth_base(seed, tensor_id(l, T_UP)), -7, m->st))) return rc;
+    if ((rc = qlinear_synth(L.down, 0, 1, H, synth_base(seed, tensor_id(l, T_DOWN)), -7, m->st))) return rc;
+    auto w = synth_norm(seed, tensor_id(l, T_IN_NORM), H);
+    MC_HIP(hipMemcpy(L.in_norm, w.data(), (size_t)H * 2, hipMemcpyHostToDevice));
+    w = synth_norm(seed, tensor_id(l, T_POST_NORM), H);
+    MC_HIP(hipMemcpy(L.post_norm, w.data(), (size_t)H * 2, hipMemcpyHostToDevice));
+    if (L.q_norm) {
+      w = synth_norm(seed, tensor_id(l, T_Q_NORM), d);
+      MC_HIP(hipMemcpy(L.q_norm, w.data(), (size_t)d * 2, hipMemcpyHostToDevice));
+      w = synth_norm(seed, tensor_id(l, T_K_NORM), d);
+      MC_HIP(hipMemcpy(L.k_norm, w.data(), (size_t)d * 2, hipMemcpyHostToDevice));
+    }
+  }
+  if ((rc = qlinear_synth(m->embed, 0, 1, c.vocab, synth_base(seed, TID_EMBED), -7, m->st))) return rc;
+  if (!c.tied_embeddings && (rc = qlinear_synth(m->lm_head, 0, 1, c.vocab, synth_base(seed, TID_LM_HEAD), -7, m->st)))
+    return rc;
+  auto w = synth_norm(seed, TID_FINAL_NORM, H);
+  MC_HIP(hipMemcpy(m->final_norm, w.data(), (size_t)H * 2, hipMemcpyHostToDevice));
+  MC_HIP(hipStreamSynchronize(m->st));
+  return MC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// batch
+// ---------------------------------------------------------------------------
+struct mc_batch {
+  mc_model* m = nullptr;
+  int R = 0, cap = 0, K = 0, K1 = 1, hcap = 0, Mmax = 0;
+  mc_spec_config spec{};
+  hipStream_t st = nullptr;
+  std::vector<KVLayer> kv;
+  uint16_t* kv_mem = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  uint16_t *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *act = nullptr,
+           *logits = nullptr;
+  float* gemv_part = nullptr;
+  unsigned* gemv_cnt = nullptr;
+  AttnWork aw{};
+  StepState s;
+  void* scratch = nullptr;  // one allocation for the small StepState arrays
+  // pinned staging
+  int32_t* h_i32 = nullptr;  // general staging
+  size_t h_i32_n = 0;
+  int32_t* h_out = nullptr;  // [R*K1 tok | R cnt | R fin | R nprop | R kv_len]
+  hipGraphExec_t graph = nullptr;
+  hipGraph_t graph_def = nullptr;
+  std::vector<int32_t> widths;
+  std::vector<int32_t> kv_len_host;
+  uint64_t unseeded = 0;
+  // profiling
+  bool profiling = false;
+  std::vector<hipEvent_t> ev;
+  size_t ev_used = 0;
+  struct Rec { int kind; size_t e0, e1; double bytes; };
+  std::vector<Rec> recs;
+  double prof_ms[3] = {0, 0, 0}, prof_bytes[3] = {0, 0, 0};
+  int prof_launch[3] = {0, 0, 0};
+};
+
+static void batch_free(mc_batch* b) {
+  if (!b) return;
+  (void)hipSetDevice(b->m->device);
+  if (b->graph) (void)hipGraphExecDestroy(b->graph);
+  if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
+  for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->xn, (void*)b->qkv,
+                  (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
+                  (void*)b->gemv_cnt, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
+    if (p) (void)hipFree(p);
+  if (b->h_i32) (void)hipHostFree(b->h_i32);
+  if (b->h_out) (void)hipHostFree(b->h_out);
+  for (auto e : b->ev) (void)hipEventDestroy(e);
+  if (b->st) (void)hipStreamDestroy(b->st);
+  delete b;
+}
+
+extern "C" void mc_batch_destroy(mc_batch* b) { batch_free(b); }
+
+static int stage_i32(mc_batch* b, size_t n) {
+  if (n <= b->h_i32_n) return MC_OK;
+  if (b->h_i32) MC_HIP(hipHostFree(b->h_i32));
+  b->h_i32 = nullptr;
+  MC_HIP(hipHostMalloc((void**)&b->h_i32, n * 4, hipHostMallocDefault));
+  b->h_i32_n = n;
+  return MC_OK;
+}
+
+extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, int32_t max_draft,
+                               const mc_spec_config* spec, mc_batch** out) {
+  if (!m || !out || !spec) return fail(MC_E_INVALID, "mc_batch_create: null argument");
+  if (max_rows <= 0 || max_rows > 1024 || max_ctx <= 1 || max_draft < 0 || max_draft > 64)
+    return fail(MC_E_INVALID, "mc_batch_create: bad sizes");
+  *out = nullptr;
+  MC_HIP(hipSetDevice(m->device));
+  auto* b = new mc_batch();
+  b->m = m;
+  b->spec = *spec;
+  if (b->spec.max_proposal_tokens < 0) b->spec.max_proposal_tokens = 0;  // BatchGenerator.swift:23-25
+  if (b->spec.max_suffix_tokens < 1) b->spec.max_suffix_tokens = 1;
+  if (b->spec.min_context_tokens < 2) b->spec.min_context_tokens = 2;
+  if (b->spec.max_proposal_tokens > max_draft) b->spec.max_proposal_tokens = max_draft;
+  b->R = max_rows;
+  b->cap = max_ctx;
+  b->K = b->spec.enabled ? b->spec.max_proposal_tokens : 0;
+  b->K1 = b->K + 1;
+  b->hcap = max_ctx + b->K1 + 1;
+  b->Mmax = std::max(b->R * b->K1, PREFILL_CHUNK);
+  b->kv_len_host.assign((size_t)b->R, 0);
+  const auto& c = m->cfg;
+  int rc = MC_OK;
+  MC_HIP(hipStreamCreateWithFlags(&b->st, hipStreamNonBlocking));
+  const int V = c.vocab;
+  const int M = b->Mmax;
+  if (!m->fake) {
+    const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
+    const size_t per = (size_t)b->R * nkv * (size_t)max_ctx * d;
+    if ((rc = dev_zero(&b->kv_mem, per * 2 * (size_t)c.n_layers))) { batch_free(b); return rc; }
+    b->kv.resize((size_t)c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+      b->kv[(size_t)l].k = b->kv_mem + per * 2 * (size_t)l;
+      b->kv[(size_t)l].v = b->kv_mem + per * (2 * (size_t)l + 1);
+      b->kv[(size_t)l].cap = max_ctx;
+    }
+    // RoPE table in double precision, rounded to float (shared definition with the oracle)
+    const int hd = d / 2;
+    std::vector<float> cs((size_t)max_ctx * hd), sn((size_t)max_ctx * hd);
+    for (int p = 0; p < max_ctx; ++p)
+      for (int i = 0; i < hd; ++i) {
+        const double inv = std::pow((double)c.rope_theta, -2.0 * (double)i / (double)d);
+        const double a = (double)p * inv;
+        cs[(size_t)p * hd + i] = (float)std::cos(a);
+        sn[(size_t)p * hd + i] = (float)std::sin(a);
+      }
+    if ((rc = dev_alloc(&b->rope_cos, cs.size())) || (rc = dev_alloc(&b->rope_sin, sn.size()))) { batch_free(b); return rc; }
+    MC_HIP(hipMemcpy(b->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    MC_HIP(hipMemcpy(b->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    const size_t Nqkv = (size_t)(nq + 2 * nkv) * d;
+    if ((rc = dev_zero(&b->x, (size_t)M * H)) || (rc = dev_zero(&b->xn, (size_t)M * std::max(H, I))) ||
+        (rc = dev_zero(&b->qkv, (size_t)M * Nqkv)) || (rc = dev_zero(&b->q, (size_t)M * nq * d)) ||
+        (rc = dev_zero(&b->att, (size_t)M * nq * d)) || (rc = dev_zero(&b->act, (size_t)M * I))) {
+      batch_free(b);
+      return rc;
+    }
+    // split-K workspace: the largest plan over every linear and m-tile class
+    size_t part = 1;
+    int maxnt = 1;
+    auto acc_plan = [&](const QLinear& L) {
+      for (int MT = 1; MT <= 4; ++MT) {
+        int gpr, ks;
+        gemv_plan(L, MT, &gpr, &ks);
+        if (ks > 1) part = std::max(part, (size_t)ks * L.NT * MT * 64 * 4);
+      }
+      maxnt = std::max(maxnt, L.NT);
+    };
+    for (auto& L : m->layers) { acc_plan(L.qkv); acc_plan(L.o); acc_plan(L.gateup); acc_plan(L.down); }
+    acc_plan(m->head());
+    if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt))) { batch_free(b); return rc; }
+    b->aw.nchunk = (max_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    if ((rc = dev_alloc(&b->aw.part_o, (size_t)M * nq * b->aw.nchunk * d)) ||
+        (rc = dev_alloc(&b->aw.part_ml, (size_t)M * nq * b->aw.nchunk * 2))) {
+      batch_free(b);
+      return rc;
+    }
+  }
+  if ((rc = dev_zero(&b->logits, (size_t)M * V))) { batch_free(b); return rc; }
+
+  // small per-row state in one zeroed allocation
+  StepState& s = b->s;
+  s.R = b->R; s.K = b->K; s.K1 = b->K1; s.hcap = b->hcap; s.V = V;
+  s.enabled = b->spec.enabled; s.max_suffix = b->spec.max_suffix_tokens; s.min_ctx = b->spec.min_context_tokens;
+  s.acceptance = b->spec.acceptance; s.single_row_only = b->spec.single_row_only; s.greedy_only = b->spec.greedy_only;
+  const size_t R = (size_t)b->R, RK = R * b->K1, Ms = (size_t)M;
+  size_t words = 0;
+  auto take = [&](size_t n) { size_t o = words; words += (n + 1) & ~(size_t)1; return o; };  // 8-byte aligned in u32 units
+  const size_t o_active = take(R), o_hist = take(R * b->hcap), o_hlen = take(R), o_gen = take(R), o_max = take(R),
+               o_cur = take(R), o_kv = take(R), o_temp = take(R), o_topp = take(R), o_invt = take(R),
+               o_hseed = take(R), o_seed = take(2 * R), o_ctr = take(2 * R), o_eos = take(8 * R), o_neos = take(R),
+               o_rej = take(R), o_dr = take(RK), o_np = take(R), o_stok = take(Ms), o_srow = take(Ms),
+               o_spos = take(Ms), o_rs0 = take(R), o_nv = take(R), o_qb = take(R), o_sct = take(RK),
+               o_sca = take(RK), o_scr = take(RK), o_forced = take(R), o_otok = take(RK), o_ocnt = take(R),
+               o_ofin = take(R), o_stats = take(8);
+  uint32_t* base;
+  if ((rc = dev_zero(&base, words))) { batch_free(b); return rc; }
+  b->scratch = base;
+  auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(base + o); };
+  s.active = I32(o_active); s.hist = I32(o_hist); s.hist_len = I32(o_hlen); s.gen = I32(o_gen); s.max_gen = I32(o_max);
+  s.cur = I32(o_cur); s.kv_len = I32(o_kv); s.temp = reinterpret_cast<float*>(base + o_temp);
+  s.top_p = reinterpret_cast<float*>(base + o_topp); s.inv_temp = reinterpret_cast<float*>(base + o_invt);
+  s.has_seed = I32(o_hseed); s.seed = reinterpret_cast<uint64_t*>(base + o_seed);
+  s.counter = reinterpret_cast<uint64_t*>(base + o_ctr); s.eos = I32(o_eos); s.n_eos = I32(o_neos);
+  s.reject = I32(o_rej); s.drafts = I32(o_dr); s.nprop = I32(o_np); s.slot_tok = I32(o_stok);
+  s.slot_row = I32(o_srow); s.slot_pos = I32(o_spos); s.row_slot0 = I32(o_rs0); s.n_valid = I32(o_nv);
+  s.qbase = I32(o_qb); s.scan_tok = I32(o_sct); s.scan_acc = I32(o_sca); s.scan_res = I32(o_scr);
+  s.forced = I32(o_forced); s.out_tok = I32(o_otok); s.out_cnt = I32(o_ocnt); s.out_fin = I32(o_ofin);
+  s.stats = reinterpret_cast<unsigned long long*>(base + o_stats);
+  // forced = -1 (none), reject = -1
+  {
+    std::vector<int32_t> neg(R, -1);
+    MC_HIP(hipMemcpy(s.forced, neg.data(), R * 4, hipMemcpyHostToDevice));
+    MC_HIP(hipMemcpy(s.reject, neg.data(), R * 4, hipMemcpyHostToDevice));
+  }
+  if ((rc = stage_i32(b, std::max<size_t>(4096, (size_t)b->hcap + 16)))) { batch_free(b); return rc; }
+  MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R) * 4, hipHostMallocDefault));
+  *out = b;
+  return MC_OK;
+}
+
+// --------------------------- forward --------------------------------------
+static int prof_begin(mc_batch* b, size_t* e0) {
+  if (!b->profiling) return MC_OK;
+  if (b->ev_used + 2 > b->ev.size()) {
+    for (int i = 0; i < 64; ++i) {
+      hipEvent_t e;
+      MC_HIP(hipEventCreate(&e));
+      b->ev.push_back(e);
+    }
+  }
+  *e0 = b->ev_used++;
+  MC_HIP(hipEventRecord(b->ev[*e0], b->st));
+  return MC_OK;
+}
+static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
+  if (!b->profiling) return MC_OK;
+  const size_t e1 = b->ev_used++;
+  MC_HIP(hipEventRecord(b->ev[e1], b->st));
+  b->recs.push_back({kind, e0, e1, bytes});
+  return MC_OK;
+}
+
+static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, uint16_t* y, int ldy, int M, int epi) {
+  for (int m0 = 0; m0 < M; m0 += 64) {
+    const int mc = std::min(64, M - m0);
+    const int MT = (mc + 15) / 16;
+    GemvArgs a;
+    a.qw = L.qw; a.sb = L.sb;
+    a.x = x + (size_t)m0 * ldx; a.ldx = ldx;
+    a.y = y + (size_t)m0 * ldy; a.ldy = ldy;
+    a.M = mc; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
+    gemv_plan(L, MT, &a.gpr, &a.ksplit);
+    a.part = b->gemv_part; a.counters = b->gemv_cnt; a.epi = epi;
+    size_t e0 = 0;
+    int rc = prof_begin(b, &e0);
+    if (rc) return rc;
+    if ((rc = gemv_launch(a, MT, b->st))) return rc;
+    if ((rc = prof_end(b, e0, 0, L.alg_bytes()))) return rc;
+  }
+  return MC_OK;
+}
+
+// Forward over M slots already described in the StepState slot arrays.  Logits are
+// produced for slots [lg0, lg0 + lgn) into b->logits rows [lg0, lg0 + lgn).
+static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
+  mc_model* m = b->m;
+  const auto& c = m->cfg;
+  const StepState& s = b->s;
+  int rc;
+  if (m->fake) {
+    if (lgn > 0) return launch_fake_logits(c.arch, s.slot_tok + lg0, lgn, c.vocab, b->logits + (size_t)lg0 * c.vocab, b->st);
+    return MC_OK;
+  }
+  const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
+  const int Nqkv = (nq + 2 * nkv) * d;
+  SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
+  if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->st))) return rc;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const auto& L = m->layers[(size_t)l];
+    if ((rc = launch_rmsnorm(b->x, L.in_norm, M, H, c.rms_eps, b->xn, b->st))) return rc;
+    if ((rc = run_gemv(b, L.qkv, b->xn, H, b->qkv, Nqkv, M, EPI_STORE))) return rc;
+    if ((rc = launch_qk_rope_append(b->qkv, L.q_norm, L.k_norm, b->rope_cos, b->rope_sin, M, nq, nkv, d, c.rms_eps,
+                                    s.slot_row, s.slot_pos, b->kv[(size_t)l], b->q, b->st)))
+      return rc;
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    if ((rc = launch_attention(b->q, b->kv[(size_t)l], sv, b->R, max_q, nq, nkv, d, M, b->aw, b->att, b->st)))
+      return rc;
+    if ((rc = prof_end(b, e0, 1, 0.0))) return rc;
+    if ((rc = run_gemv(b, L.o, b->att, nq * d, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if ((rc = launch_rmsnorm(b->x, L.post_norm, M, H, c.rms_eps, b->xn, b->st))) return rc;
+    if ((rc = run_gemv(b, L.gateup, b->xn, H, b->act, I, M, EPI_SWIGLU))) return rc;
+    if ((rc = run_gemv(b, L.down, b->act, I, b->x, H, M, EPI_RESIDUAL))) return rc;
+  }
+  if (lgn > 0) {
+    if ((rc = launch_rmsnorm(b->x + (size_t)lg0 * H, m->final_norm, lgn, H, c.rms_eps, b->xn, b->st))) return rc;
+    if ((rc = run_gemv(b, m->head(), b->xn, H, b->logits + (size_t)lg0 * c.vocab, c.vocab, lgn, EPI_STORE))) return rc;
+  }
+  return MC_OK;
+}
+
+static int upload_i32(mc_batch* b, int32_t* dst, const int32_t* src, size_t n) {
+  int rc = stage_i32(b, n);
+  if (rc) return rc;
+  MC_HIP(hipStreamSynchronize(b->st));  // staging buffer reuse
+  memcpy(b->h_i32, src, n * 4);
+  MC_HIP(hipMemcpyAsync(dst, b->h_i32, n * 4, hipMemcpyHostToDevice, b->st));
+  MC_HIP(hipStreamSynchronize(b->st));
+  return MC_OK;
+}
+
+// Describe counts[i] new tokens of rows[i] as slots (packed), with qbase = kv_len.
+static int set_slots(mc_batch* b, int nrows, const int32_t* rows, const int32_t* counts, const int32_t* tokens, int* M) {
+  const int R = b->R;
+  int total = 0;
+  for (int i = 0; i < nrows; ++i) total += counts[i];
+  std::vector<int32_t> tok((size_t)total), row((size_t)total), pos((size_t)total), rs0((size_t)R, 0), nv((size_t)R, 0),
+      qb((size_t)R, 0);
+  for (int r = 0; r < R; ++r) qb[(size_t)r] = b->kv_len_host[(size_t)r];
+  int o = 0;
+  for (int i = 0; i < nrows; ++i) {
+    const int r = rows[i];
+    rs0[(size_t)r] = o;
+    nv[(size_t)r] = counts[i];
+    for (int j = 0; j < counts[i]; ++j, ++o) {
+      tok[(size_t)o] = tokens[o];
+      row[(size_t)o] = r;
+      pos[(size_t)o] = b->kv_len_host[(size_t)r] + j;
+    }
+  }
+  int rc;
+  if ((rc = upload_i32(b, b->s.slot_tok, tok.data(), tok.size()))) return rc;
+  if ((rc = upload_i32(b, b->s.slot_row, row.data(), row.size()))) return rc;
+  if ((rc = upload_i32(b, b->s.slot_pos, pos.data(), pos.size()))) return rc;
+  if ((rc = upload_i32(b, b->s.row_slot0, rs0.data(), rs0.size()))) return rc;
+  if ((rc = upload_i32(b, b->s.n_valid, nv.data(), nv.size()))) return rc;
+  if ((rc = upload_i32(b, b->s.qbase, qb.data(), qb.size()))) return rc;
+  *M = total;
+  return MC_OK;
+}
+
+static int set_row_i32(mc_batch* b, int32_t* arr, int row, int32_t v) { return upload_i32(b, arr + row, &v, 1); }
+
+static int sync_kv_len(mc_batch* b) {
+  MC_HIP(hipStreamSynchronize(b->st));
+  MC_HIP(hipMemcpy(b->kv_len_host.data(), b->s.kv_len, (size_t)b->R * 4, hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
+extern "C" int mc_forward(mc_batch* b, int32_t nrows, const int32_t* rows, const int32_t* counts,
+                          const int32_t* tokens, uint16_t* logits_host) {
+  if (!b || (nrows > 0 && (!rows || !counts || !tokens))) return fail(MC_E_INVALID, "mc_forward: null argument");
+  MC_HIP(hipSetDevice(b->m->device));
+  int rc = sync_kv_len(b);
+  if (rc) return rc;
+  int total = 0;
+  std::vector<int> seen((size_t)b->R, 0);
+  for (int i = 0; i < nrows; ++i) {
+    const int r = rows[i];
+    if (r < 0 || r >= b->R || seen[(size_t)r]++) return fail(MC_E_INVALID, "mc_forward: bad or repeated row");
+    if (counts[i] < 0) return fail(MC_E_INVALID, "mc_forward: negative count");
+    if (b->kv_len_host[(size_t)r] + counts[i] > b->cap) return fail(MC_E_CAPACITY, "mc_forward: context capacity exceeded");
+    total += counts[i];
+  }
+  if (total == 0) return MC_OK;
+  if (total > b->Mmax) return fail(MC_E_CAPACITY, "mc_forward: too many tokens for one call");
+  int M;
+  if ((rc = set_slots(b, nrows, rows, counts, tokens, &M))) return rc;
+  int maxq = 0;
+  for (int i = 0; i < nrows; ++i) maxq = std::max(maxq, (int)counts[i]);
+  if ((rc = forward_slots(b, M, maxq, 0, logits_host ? M : 0))) return rc;
+  // advance kv_len
+  for (int i = 0; i < nrows; ++i) b->kv_len_host[(size_t)rows[i]] += counts[i];
+  if ((rc = upload_i32(b, b->s.kv_len, b->kv_len_host.data(), (size_t)b->R))) return rc;
+  if (logits_host) {
+    MC_HIP(hipMemcpyAsync(logits_host, b->logits, (size_t)M * b->m->cfg.vocab * 2, hipMemcpyDeviceToHost, b->st));
+  }
+  MC_HIP(hipStreamSynchronize(b->st));
+  return MC_OK;
+}
+
+// --------------------------- admission ------------------------------------
+static int set_row_sampling(mc_batch* b, int row, const mc_sampling* sp) {
+  StepState& s = b->s;
+  const float t = sp->temperature;
+  const float inv = t != 0.0f ? 1.0f / t : 0.0f;
+  int32_t rowv[16];
+  int rc;
+  memcpy(&rowv[0], &t, 4);
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.temp) + row, rowv, 1))) return rc;
+  memcpy(&rowv[0], &sp->top_p, 4);
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.top_p) + row, rowv, 1))) return rc;
+  memcpy(&rowv[0], &inv, 4);
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.inv_temp) + row, rowv, 1))) return rc;
+  if ((rc = set_row_i32(b, s.has_seed, row, sp->has_seed ? 1 : 0))) return rc;
+  // unseeded rows: a per-batch stream keyed by admission order (global seed 7)
+  const uint64_t seed = sp->has_seed ? sp->seed : mix64(7ull ^ mix64(++b->unseeded));
+  uint64_t two[2] = {seed, 0};
+  memcpy(rowv, two, 16);
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.seed + row), rowv, 2))) return rc;
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.counter + row), rowv + 2, 2))) return rc;
+  int32_t eos[8] = {0};
+  const int ne = std::max(0, std::min(8, sp->n_eos));
+  for (int i = 0; i < ne; ++i) eos[i] = sp->eos[i];
+  if ((rc = upload_i32(b, s.eos + row * 8, eos, 8))) return rc;
+  if ((rc = set_row_i32(b, s.n_eos, row, ne))) return rc;
+  return set_row_i32(b, s.reject, row, sp->reject_token);
+}
+
+static int check_row(mc_batch* b, int row) {
+  if (row < 0 || row >= b->R) return fail(MC_E_INVALID, "row out of range");
+  return MC_OK;
+}
+
+extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
+                               const mc_sampling* sp, int32_t* first_token, int32_t* finished) {
+  if (!b || !prompt || !sp || n_prompt < 1 || max_tokens < 1) return fail(MC_E_INVALID, "mc_batch_insert: bad argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if ((size_t)n_prompt + (size_t)max_tokens + (size_t)b->K1 + 1 > (size_t)b->cap)
+    return fail(MC_E_CAPACITY, "mc_batch_insert: prompt + max_tokens exceeds the context capacity");
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  StepState& s = b->s;
+  const int V = b->m->cfg.vocab;
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= V) return fail(MC_E_INVALID, "mc_batch_insert: token id out of range");
+  if ((rc = set_row_i32(b, s.active, row, 0))) return rc;
+  b->kv_len_host[(size_t)row] = 0;
+  // prefill all but the last prompt token (Scheduler.swift:722-739), in chunks
+  int done = 0;
+  while (done < n_prompt - 1) {
+    const int cnt = std::min(PREFILL_CHUNK, n_prompt - 1 - done);
+    int M;
+    if ((rc = set_slots(b, 1, &row, &cnt, prompt + done, &M))) return rc;
+    if ((rc = forward_slots(b, M, cnt, 0, 0))) return rc;
+    b->kv_len_host[(size_t)row] += cnt;
+    done += cnt;
+  }
+  if (n_prompt > 1) b->widths.push_back(1);
+  // last prompt token with logits, then first-token sampling through the acceptance kernels
+  {
+    const int one = 1;
+    int M;
+    if ((rc = set_slots(b, 1, &row, &one, prompt + n_prompt - 1, &M))) return rc;
+    if ((rc = forward_slots(b, M, 1, 0, 1))) return rc;
+  }
+  if ((rc = upload_i32(b, s.hist + (size_t)row * b->hcap, prompt, (size_t)n_prompt))) return rc;
+  if ((rc = set_row_i32(b, s.hist_len, row, n_prompt))) return rc;
+  if ((rc = set_row_i32(b, s.gen, row, 0))) return rc;
+  if ((rc = set_row_i32(b, s.max_gen, row, max_tokens))) return rc;
+  if ((rc = set_row_i32(b, s.cur, row, prompt[n_prompt - 1]))) return rc;
+  if ((rc = set_row_i32(b, s.kv_len, row, n_prompt - 1))) return rc;
+  if ((rc = set_row_i32(b, s.nprop, row, 0))) return rc;
+  if ((rc = set_row_sampling(b, row, sp))) return rc;
+  if ((rc = set_row_i32(b, s.active, row, 1))) return rc;
+  if ((rc = launch_accept_scan(s, b->logits, row, b->st))) return rc;
+  if ((rc = launch_commit(s, row, b->st))) return rc;
+  int32_t res[2];
+  MC_HIP(hipMemcpyAsync(&res[0], s.out_tok + (size_t)row * b->K1, 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipMemcpyAsync(&res[1], s.out_fin + row, 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipStreamSynchronize(b->st));
+  b->kv_len_host[(size_t)row] = n_prompt;
+  if (first_token) *first_token = res[0];
+  if (finished) *finished = res[1];
+  return MC_OK;
+}
+
+extern "C" int mc_batch_fill_synthetic_kv(mc_batch* b, int32_t row, int32_t n, uint64_t seed) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if (n < 0 || n > b->cap) return fail(MC_E_CAPACITY, "fill_synthetic_kv: n exceeds capacity");
+  MC_HIP(hipSetDevice(b->m->device));
+  const auto& c = b->m->cfg;
+  if (!b->m->fake)
+    for (int l = 0; l < c.n_layers; ++l)
+      if ((rc = launch_kv_synth(b->kv[(size_t)l], l, row, c.n_kv_heads, c.head_dim, n, seed, b->st))) return rc;
+  if ((rc = set_row_i32(b, b->s.kv_len, row, n))) return rc;
+  b->kv_len_host[(size_t)row] = n;
+  MC_HIP(hipStreamSynchronize(b->st));
+  return MC_OK;
+}
+
+extern "C" int mc_batch_insert_prefilled(mc_batch* b, int32_t row, const int32_t* ctx, int32_t n_ctx,
+                                         int32_t max_tokens, const mc_sampling* sp) {
+  if (!b || !ctx || !sp || n_ctx < 1 || max_tokens < 1) return fail(MC_E_INVALID, "insert_prefilled: bad argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  if (b->kv_len_host[(size_t)row] != n_ctx - 1) return fail(MC_E_STATE, "insert_prefilled: kv_len must equal n_ctx - 1");
+  if ((size_t)n_ctx + (size_t)max_tokens + (size_t)b->K1 + 1 > (size_t)b->cap)
+    return fail(MC_E_CAPACITY, "insert_prefilled: context + max_tokens exceeds capacity");
+  StepState& s = b->s;
+  if ((rc = upload_i32(b, s.hist + (size_t)row * b->hcap, ctx, (size_t)n_ctx))) return rc;
+  if ((rc = set_row_i32(b, s.hist_len, row, n_ctx))) return rc;
+  if ((rc = set_row_i32(b, s.gen, row, 1))) return rc;
+  if ((rc = set_row_i32(b, s.max_gen, row, max_tokens))) return rc;
+  if ((rc = set_row_i32(b, s.cur, row, ctx[n_ctx - 1]))) return rc;
+  if ((rc = set_row_sampling(b, row, sp))) return rc;
+  return set_row_i32(b, s.active, row, 1);
+}
+
+extern "C" int mc_batch_remove(mc_batch* b, int32_t row) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  MC_HIP(hipSetDevice(b->m->device));
+  return set_row_i32(b, b->s.active, row, 0);
+}
+
+extern "C" int mc_batch_rollback(mc_batch* b, int32_t row, int32_t n) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if (n < 0) return fail(MC_E_INVALID, "rollback: negative count");
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  const int len = b->kv_len_host[(size_t)row];
+  b->kv_len_host[(size_t)row] = len - std::min(n, len);
+  return set_row_i32(b, b->s.kv_len, row, b->kv_len_host[(size_t)row]);
+}
+
+extern "C" int mc_batch_trim(mc_batch* b, int32_t n) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  if (n < 0) return fail(MC_E_INVALID, "trim: negative count");
+  MC_HIP(hipSetDevice(b->m->device));
+  int rc = sync_kv_len(b);
+  if (rc) return rc;
+  int idx = 0;
+  for (int v : b->kv_len_host) idx = std::max(idx, v);
+  const int trimmed = std::min(idx, n);  // BatchCache.swift:406
+  if (trimmed <= 0) return 0;
+  for (auto& v : b->kv_len_host) v -= std::min(trimmed, v);  // per-row: min(trimmed, row length)
+  if ((rc = upload_i32(b, b->s.kv_len, b->kv_len_host.data(), (size_t)b->R))) return rc;
+  return trimmed;
+}
+
+extern "C" int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len) {
+  if (!b || !len) return fail(MC_E_INVALID, "null argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  *len = b->kv_len_host[(size_t)row];
+  return MC_OK;
+}
+
+extern "C" int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t which_v, uint16_t* out) {
+  if (!b || !out) return fail(MC_E_INVALID, "null argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if (b->m->fake) return fail(MC_E_STATE, "fake model has no KV");
+  const auto& c = b->m->cfg;
+  if (layer < 0 || layer >= c.n_layers) return fail(MC_E_INVALID, "layer out of range");
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  const int len = b->kv_len_host[(size_t)row];
+  const uint16_t* src = which_v ? b->kv[(size_t)layer].v : b->kv[(size_t)layer].k;
+  for (int h = 0; h < c.n_kv_heads; ++h)
+    MC_HIP(hipMemcpy(out + (size_t)h * len * c.head_dim,
+                     src + (((size_t)row * c.n_kv_heads + h) * b->cap) * c.head_dim, (size_t)len * c.head_dim * 2,
+                     hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
+extern "C" int mc_batch_history(mc_batch* b, int32_t row, int32_t* out, int32_t cap, int32_t* len) {
+  if (!b || !len) return fail(MC_E_INVALID, "null argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  MC_HIP(hipSetDevice(b->m->device));
+  MC_HIP(hipStreamSynchronize(b->st));
+  int32_t n = 0;
+  MC_HIP(hipMemcpy(&n, b->s.hist_len + row, 4, hipMemcpyDeviceToHost));
+  *len = n;
+  if (out && cap > 0)
+    MC_HIP(hipMemcpy(out, b->s.hist + (size_t)row * b->hcap, (size_t)std::min(n, cap) * 4, hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
+// --------------------------- the step -------------------------------------
+static int enqueue_step(mc_batch* b) {
+  int rc;
+  const StepState& s = b->s;
+  if ((rc = launch_propose(s, b->st))) return rc;
+  const int M = b->R * b->K1;
+  if ((rc = forward_slots(b, M, b->K1, 0, M))) return rc;
+  if ((rc = launch_accept_scan(s, b->logits, -1, b->st))) return rc;
+  return launch_commit(s, -1, b->st);
+}
+
+extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_tokens, int32_t* out_counts,
+                       int32_t* out_finish) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  MC_HIP(hipSetDevice(b->m->device));
+  int rc;
+  const int R = b->R, K1 = b->K1;
+  // forced accept-length schedule (or none)
+  {
+    std::vector<int32_t> f((size_t)R, -1);
+    if (forced_accept)
+      for (int r = 0; r < R; ++r) f[(size_t)r] = forced_accept[r] < 0 ? -1 : forced_accept[r];
+    if ((rc = upload_i32(b, b->s.forced, f.data(), (size_t)R))) return rc;
+  }
+  if (b->profiling) {
+    b->ev_used = 0;
+    b->recs.clear();
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    if ((rc = enqueue_step(b))) return rc;
+    if ((rc = prof_end(b, e0, 2, 0.0))) return rc;
+  } else {
+    if (!b->graph) {
+      MC_HIP(hipStreamBeginCapture(b->st, hipStreamCaptureModeThreadLocal));
+      rc = enqueue_step(b);
+      hipGraph_t g = nullptr;
+      hipError_t e = hipStreamEndCapture(b->st, &g);
+      if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+      b->graph_def = g;
+      MC_HIP(hipGraphInstantiate(&b->graph, g, nullptr, nullptr, 0));
+    }
+    MC_HIP(hipGraphLaunch(b->graph, b->st));
+  }
+  const StepState& s = b->s;
+  int32_t* h = b->h_out;
+  MC_HIP(hipMemcpyAsync(h, s.out_tok, (size_t)R * K1 * 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipMemcpyAsync(h + R * K1, s.out_cnt, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipMemcpyAsync(h + R * K1 + R, s.out_fin, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipMemcpyAsync(h + R * K1 + 2 * R, s.nprop, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipMemcpyAsync(h + R * K1 + 3 * R, s.kv_len, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  MC_HIP(hipStreamSynchronize(b->st));
+  if (out_tokens) memcpy(out_tokens, h, (size_t)R * K1 * 4);
+  if (out_counts) memcpy(out_counts, h + R * K1, (size_t)R * 4);
+  if (out_finish) memcpy(out_finish, h + R * K1 + R, (size_t)R * 4);
+  for (int r = 0; r < R; ++r) {
+    if (h[R * K1 + r] > 0) b->widths.push_back(h[R * K1 + 2 * R + r] + 1);
+    b->kv_len_host[(size_t)r] = h[R * K1 + 3 * R + r];
+  }
+  if (b->profiling) {
+    for (int k = 0; k < 3; ++k) { b->prof_ms[k] = 0; b->prof_bytes[k] = 0; b->prof_launch[k] = 0; }
+    for (const auto& rec : b->recs) {
+      float ms = 0;
+      MC_HIP(hipEventElapsedTime(&ms, b->ev[rec.e0], b->ev[rec.e1]));
+      b->prof_ms[rec.kind] += ms;
+      b->prof_bytes[rec.kind] += rec.bytes;
+      b->prof_launch[rec.kind] += 1;
+    }
+  }
+  return MC_OK;
+}
+
+extern "C" int mc_batch_stats(mc_batch* b, mc_spec_stats* out) {
+  if (!b || !out) return fail(MC_E_INVALID, "null argument");
+  MC_HIP(hipSetDevice(b->m->device));
+  MC_HIP(hipStreamSynchronize(b->st));
+  unsigned long long v[4];
+  MC_HIP(hipMemcpy(v, b->s.stats, sizeof v, hipMemcpyDeviceToHost));
+  out->proposed = (int64_t)v[0];
+  out->accepted = (int64_t)v[1];
+  out->proposal_batches = (int64_t)v[2];
+  out->rejected_batches = (int64_t)v[3];
+  return MC_OK;
+}
+
+extern "C" int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  const int n = (int)b->widths.size();
+  for (int i = 0; i < n && i < cap && out; ++i) out[i] = b->widths[(size_t)i];
+  return n;
+}
+
+extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
+  if (!b) return fail(MC_E_INVALID, "null batch");
+  b->profiling = enabled != 0;
+  return MC_OK;
+}
+
+extern "C" int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches) {
+  if (!b || kind < 0 || kind > 2) return fail(MC_E_INVALID, "bad argument");
+  if (ms) *ms = b->prof_ms[kind];
+  if (bytes) *bytes = b->prof_bytes[kind];
+  if (launches) *launches = b->prof_launch[kind];
+  return MC_OK;
+}
+
+// --------------------------- standalone proposer / acceptance -------------
+extern "C" int mc_ngram_propose(const int32_t* hist, const int64_t* hist_off, int32_t B, int32_t max_suffix,
+                                int32_t min_context, const int32_t* limit, int32_t out_stride, int32_t* out,
+                                int32_t* out_len) {
+  if (!hist_off || !limit || !out || !out_len || B < 0) return fail(MC_E_INVALID, "mc_ngram_propose: null argument");
+  if (B == 0) return MC_OK;
+  for (int r = 0; r < B; ++r)
+    if (limit[r] > out_stride || hist_off[r + 1] < hist_off[r]) return fail(MC_E_INVALID, "mc_ngram_propose: bad limit/offsets");
+  max_suffix = std::max(1, max_suffix);
+  min_context = std::max(2, min_context);
+  MC_HIP(hipSetDevice(g_device));
+  const size_t nh = (size_t)hist_off[B];
+  int32_t *dh = nullptr, *dl = nullptr, *dout = nullptr, *dlen = nullptr;
+  int64_t* doff = nullptr;
+  int rc = MC_OK;
+  hipStream_t st;
+  MC_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  if (!(rc = dev_alloc(&dh, nh)) && !(rc = dev_alloc(&doff, (size_t)B + 1)) && !(rc = dev_alloc(&dl, (size_t)B)) &&
+      !(rc = dev_alloc(&dout, (size_t)B * std::max(1, out_stride))) && !(rc = dev_alloc(&dlen, (size_t)B))) {
+    hipError_t e = hipSuccess;
+    if (nh) e = hipMemcpy(dh, hist, nh * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(doff, hist_off, ((size_t)B + 1) * 8, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dl, limit, (size_t)B * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) rc = hip_fail(e, "mc_ngram_propose upload", __FILE__, __LINE__);
+    if (!rc) rc = launch_ngram_standalone(dh, doff, B, max_suffix, min_context, dl, out_stride, dout, dlen, st);
+    if (!rc) {
+      e = hipStreamSynchronize(st);
+      if (e == hipSuccess) e = hipMemcpy(out_len, dlen, (size_t)B * 4, hipMemcpyDeviceToHost);
+      if (e == hipSuccess) e = hipMemcpy(out, dout, (size_t)B * out_stride * 4, hipMemcpyDeviceToHost);
+      if (e != hipSuccess) rc = hip_fail(e, "mc_ngram_propose", __FILE__, __LINE__);
+    }
+  }
+  for (void* p : {(void*)dh, (void*)doff, (void*)dl, (void*)dout, (void*)dlen})
+    if (p) (void)hipFree(p);
+  (void)hipStreamDestroy(st);
+  return rc;
+}
+
+extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* row_off,
+                         const int32_t* drafts, int32_t draft_stride, const int32_t* n_draft, const mc_sampling* sp,
+                         const uint64_t* counter, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
+                         int32_t* kv_keep, int32_t* n_accepted) {
+  if (!logits || !row_off || !n_draft || !sp || !counter || !out_tokens || !n_emit || !kv_keep || !n_accepted || B <= 0 ||
+      vocab <= 0)
+    return fail(MC_E_INVALID, "mc_accept: bad argument");
+  int K = 0;
+  for (int r = 0; r < B; ++r) {
+    if (n_draft[r] < 0 || n_draft[r] > draft_stride) return fail(MC_E_INVALID, "mc_accept: bad n_draft");
+    if (row_off[r + 1] - row_off[r] != n_draft[r] + 1) return fail(MC_E_INVALID, "mc_accept: row_off must give n_draft+1 rows");
+    K = std::max(K, n_draft[r]);
+  }
+  MC_HIP(hipSetDevice(g_device));
+  const int K1 = K + 1;
+  const size_t nl = (size_t)row_off[B];
+  // device state laid out as a StepState with row r's logits at slots r*K1 + j
+  StepState s;
+  s.R = B; s.K = K; s.K1 = K1; s.V = vocab; s.acceptance = acceptance; s.hcap = 1;
+  std::vector<int32_t> h_nprop((size_t)B), h_nv((size_t)B), h_rs0((size_t)B), h_act((size_t)B, 1), h_dr((size_t)B * K1, 0),
+      h_eos((size_t)B * 8, 0), h_neos((size_t)B), h_rej((size_t)B), h_hs((size_t)B), h_forced((size_t)B, -1);
+  std::vector<float> h_t((size_t)B), h_tp((size_t)B), h_it((size_t)B);
+  std::vector<uint64_t> h_seed((size_t)B), h_ctr((size_t)B);
+  for (int r = 0; r < B; ++r) {
+    h_nprop[(size_t)r] = n_draft[r];
+    h_nv[(size_t)r] = n_draft[r] + 1;
+    h_rs0[(size_t)r] = r * K1;
+    for (int j = 0; j < n_draft[r]; ++j) h_dr[(size_t)r * K1 + j] = drafts[(size_t)r * draft_stride + j];
+    const auto& q = sp[r];
+    h_t[(size_t)r] = q.temperature;
+    h_tp[(size_t)r] = q.top_p;
+    h_it[(size_t)r] = q.temperature != 0.0f ? 1.0f / q.temperature : 0.0f;
+    h_hs[(size_t)r] = q.has_seed;
+    h_seed[(size_t)r] = q.seed;
+    h_ctr[(size_t)r] = counter[r];
+    const int ne = std::max(0, std::min(8, q.n_eos));
+    for (int i = 0; i < ne; ++i) h_eos[(size_t)r * 8 + i] = q.eos[i];
+    h_neos[(size_t)r] = ne;
+    h_rej[(size_t)r] = q.reject_token;
+  }
+  std::vector<uint16_t> h_lg((size_t)B * K1 * vocab, 0);
+  for (int r = 0; r < B; ++r)
+    memcpy(&h_lg[(size_t)r * K1 * vocab], logits + (size_t)row_off[r] * vocab, (size_t)(n_draft[r] + 1) * vocab * 2);
+  (void)nl;
+  std::vector<void*> allocs;
+  int rc = MC_OK;
+  auto up = [&](auto** dst, const auto& src) -> int {
+    using T = typename std::remove_reference<decltype(src)>::type::value_type;
+    T* p = nullptr;
+    int r2 = dev_alloc(&p, src.size());
+    if (r2) return r2;
+    allocs.push_back(p);
+    MC_HIP(hipMemcpy(p, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice));
+    *dst = p;
+    return MC_OK;
+  };
+  uint16_t* dlg = nullptr;
+  int32_t *d_emit = nullptr, *d_keep = nullptr, *d_nacc = nullptr;
+  std::vector<int32_t> zeros_rk((size_t)B * K1, 0), zeros_r((size_t)B, 0);
+  if (!rc) rc = up(&dlg, h_lg);
+  if (!rc) rc = up(&s.nprop, h_nprop);
+  if (!rc) rc = up(&s.n_valid, h_nv);
+  if (!rc) rc = up(&s.row_slot0, h_rs0);
+  if (!rc) rc = up(&s.active, h_act);
+  if (!rc) rc = up(&s.drafts, h_dr);
+  if (!rc) rc = up(&s.temp, h_t);
+  if (!rc) rc = up(&s.top_p, h_tp);
+  if (!rc) rc = up(&s.inv_temp, h_it);
+  if (!rc) rc = up(&s.has_seed, h_hs);
+  if (!rc) rc = up(&s.seed, h_seed);
+  if (!rc) rc = up(&s.counter, h_ctr);
+  if (!rc) rc = up(&s.eos, h_eos);
+  if (!rc) rc = up(&s.n_eos, h_neos);
+  if (!rc) rc = up(&s.reject, h_rej);
+  if (!rc) rc = up(&s.forced, h_forced);
+  if (!rc) rc = up(&s.scan_tok, zeros_rk);
+  if (!rc) rc = up(&s.scan_acc, zeros_rk);
+  if (!rc) rc = up(&s.scan_res, zeros_rk);
+  if (!rc) rc = up(&s.out_tok, zeros_rk);
+  if (!rc) rc = up(&d_emit, zeros_r);
+  if (!rc) rc = up(&d_keep, zeros_r);
+  if (!rc) rc = up(&d_nacc, zeros_r);
+  hipStream_t st = nullptr;
+  if (!rc) {
+    hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+    if (e != hipSuccess) rc = hip_fail(e, "stream", __FILE__, __LINE__);
+  }
+  if (!rc) rc = launch_accept_scan(s, dlg, -1, st);
+  if (!rc) rc = launch_decide(s, d_emit, d_keep, d_nacc, st);
+  if (!rc) {
+    std::vector<int32_t> otok((size_t)B * K1);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = hipMemcpy(otok.data(), s.out_tok, otok.size() * 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(n_emit, d_emit, (size_t)B * 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(kv_keep, d_keep, (size_t)B * 4, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(n_accepted, d_nacc, (size_t)B * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) rc = hip_fail(e, "mc_accept", __FILE__, __LINE__);
+    if (!rc)
+      for (int r = 0; r < B; ++r)
+        for (int j = 0; j < n_emit[r]; ++j) out_tokens[(size_t)r * (draft_stride + 1) + j] = otok[(size_t)r * K1 + j];
+  }
+  if (st) (void)hipStreamDestroy(st);
+  for (void* p : allocs) (void)hipFree(p);
+  return rc;
+}

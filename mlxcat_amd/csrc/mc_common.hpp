@@ -1,0 +1,169 @@
+// mc_common.hpp -- shared definitions for the gfx950 kernels and the C-ABI host code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "../../include/mlxcat_hip.h"
+
+namespace mc {
+
+// ---------------------------------------------------------------------------
+// error plumbing
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what, const char* file, int line);
+
+#define MC_HIP(expr)                                                      \
+  do {                                                                    \
+    hipError_t _e = (expr);                                               \
+    if (_e != hipSuccess) return ::mc::hip_fail(_e, #expr, __FILE__, __LINE__); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// bf16 and hashing helpers, identical on host and device
+// ---------------------------------------------------------------------------
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t r = u + 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(r >> 16);
+}
+
+// splitmix64 finalizer (Steele, Lea, Flood 2014)
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// 32-bit uniform for (seed, per-row draw counter, position, kind); kind 0 = accept
+// test, 1 = sample draw.
+__host__ __device__ inline uint32_t uniform_u32(uint64_t seed, uint64_t counter, uint32_t pos,
+                                                uint32_t kind) {
+  uint64_t h = mix64(seed ^ 0x5851F42D4C957F2Dull);
+  h = mix64(h ^ counter);
+  h = mix64(h ^ (((uint64_t)pos << 8) | kind));
+  return (uint32_t)(h >> 32);
+}
+
+// tensor ids of the synthetic generator
+enum { T_Q = 0, T_K = 1, T_V = 2, T_O = 3, T_GATE = 4, T_UP = 5, T_DOWN = 6, T_IN_NORM = 7,
+       T_POST_NORM = 8, T_Q_NORM = 9, T_K_NORM = 10, T_ROUTER = 11 };
+inline uint64_t tensor_id(int layer, int which) { return ((uint64_t)(layer + 1) << 8) | (uint64_t)which; }
+inline uint64_t expert_tensor_id(int layer, int expert, int which) {
+  return 0x100000000ull | ((uint64_t)layer << 20) | ((uint64_t)expert << 4) | (uint64_t)which;
+}
+constexpr uint64_t TID_EMBED = 0xE0000001ull;
+constexpr uint64_t TID_LM_HEAD = 0xE0000002ull;
+constexpr uint64_t TID_FINAL_NORM = 0xE0000003ull;
+
+// ---------------------------------------------------------------------------
+// exp(x), x <= 0, with a fixed operation sequence: y = x*log2(e), n = rint(y),
+// f = y - n, 2^f by the degree-7 Taylor polynomial in (f ln2) in Horner form
+// with fused multiply-adds, exact ldexp.  Used for the integer acceptance masses
+// so that CPU and GPU decisions agree bit for bit.
+// ---------------------------------------------------------------------------
+__device__ inline float exp_neg_det(float x) {
+#pragma clang fp contract(off)
+  if (!(x > -87.0f)) return 0.0f;
+  const float LOG2E = 1.44269504088896341f;
+  float y = x * LOG2E;
+  float n = __builtin_rintf(y);
+  float f = y - n;
+  if (n < -40.0f) return 0.0f;
+  float p = 1.52527338e-05f;
+  p = __builtin_fmaf(p, f, 1.54035304e-04f);
+  p = __builtin_fmaf(p, f, 1.33335581e-03f);
+  p = __builtin_fmaf(p, f, 9.61812911e-03f);
+  p = __builtin_fmaf(p, f, 5.55041087e-02f);
+  p = __builtin_fmaf(p, f, 2.40226507e-01f);
+  p = __builtin_fmaf(p, f, 6.93147181e-01f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+__device__ inline uint64_t mass_of(float e) {
+#pragma clang fp contract(off)
+  return (uint64_t)__builtin_rintf(e * 4294967296.0f);
+}
+
+// ---------------------------------------------------------------------------
+// packed weight layout ("tile layout") for the dequant GEMV
+//
+// A linear of N outputs and K inputs is stored as NT = ceil(N/16) row tiles by
+// GP = ceil(K/128) group pairs.  Each (tile, group pair) is a 1 KiB block read by
+// one wave with one 16-byte load per lane: lane l holds row 16t + (l & 15) and
+// k-slot block c = l >> 4; its four words are [group 2gp, MFMA 0], [2gp, MFMA 1],
+// [2gp+1, MFMA 0], [2gp+1, MFMA 1].  MFMA a of group g covers physical k =
+// 64g + 32a + 8c + i, i = 0..7, i.e. exactly MLX word kw = 8g + 4a + c.  Within a
+// word, element i sits at bits 4(i/2) for even i and 16 + 4(i/2) for odd i, so
+// (w >> 4p) & 0x000F000F | 0x43004300 yields the bf16 pair (128 + q_2p, 128 + q_2p+1).
+//
+// Scales/biases: uint32 (scale bf16 | bias bf16 << 16) at
+// sb[((t * GP + gp) * 4 + c) * 8 + gi * 4 + v] for row 16t + 4c + v, group 2gp + gi,
+// which is the 4 output rows a lane holds in the MFMA accumulator layout.
+// Rows >= N and groups >= K/64 are zero (scale = bias = 0, so they add nothing).
+// ---------------------------------------------------------------------------
+struct QLinear {
+  int N = 0, K = 0, NT = 0, GP = 0;
+  uint32_t* qw = nullptr;  // NT * GP * 256 words
+  uint32_t* sb = nullptr;  // NT * GP * 32 words
+  size_t qw_words() const { return (size_t)NT * GP * 256; }
+  size_t sb_words() const { return (size_t)NT * GP * 32; }
+  // algorithmic bytes of the MLX format: N*K/2 nibbles + 4 bytes per group of 64
+  double alg_bytes() const { return (double)N * K * 0.5 + (double)N * (K / 64) * 4.0; }
+};
+
+__host__ __device__ inline uint32_t permute_mlx_word(uint32_t w) {
+  // MLX word: element i at bits 4i.  Tile word: even i at 4(i/2), odd i at 16 + 4(i/2).
+  uint32_t out = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t q = (w >> (4 * i)) & 0xFu;
+    int sh = (i & 1) ? 16 + 4 * (i >> 1) : 4 * (i >> 1);
+    out |= q << sh;
+  }
+  return out;
+}
+__host__ __device__ inline uint32_t unpermute_tile_word(uint32_t w) {
+  uint32_t out = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int sh = (i & 1) ? 16 + 4 * (i >> 1) : 4 * (i >> 1);
+    uint32_t q = (w >> sh) & 0xFu;
+    out |= q << (4 * i);
+  }
+  return out;
+}
+
+// synthetic MLX word / scale generation (matches the oracle's or_gen_linear)
+__host__ __device__ inline uint32_t synth_mlx_word(uint64_t base, int n, int KW, int kw) {
+  uint64_t idx = ((uint64_t)n * (uint64_t)KW + (uint64_t)kw) * 2u;
+  uint64_t h0 = mix64(base ^ idx), h1 = mix64(base ^ (idx + 1));
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint64_t h = j < 4 ? h0 : h1;
+    uint32_t q = (uint32_t)__builtin_popcountll((h >> (15 * (j & 3))) & 0x7FFFull);
+    w |= q << (4 * j);
+  }
+  return w;
+}
+__host__ __device__ inline uint32_t synth_scale_bias(uint64_t base, int n, int G, int g, int scale_exp) {
+  uint64_t h = mix64(base ^ 0xA5A5A5A500000000ull ^ ((uint64_t)n * (uint64_t)G + (uint64_t)g));
+  uint16_t sb = (uint16_t)(((uint32_t)(127 + scale_exp) << 7) | (0x28u + (uint32_t)(h & 0xFu)));
+  float s = bf16_to_f32(sb);
+  uint16_t bb = f32_to_bf16(-7.5f * s);
+  return (uint32_t)sb | ((uint32_t)bb << 16);
+}
+inline uint64_t synth_base(uint64_t seed, uint64_t tid) { return mix64(seed ^ mix64(tid)); }
+
+}  // namespace mc

@@ -1,0 +1,49 @@
+// mc_kernels.hpp -- launch interface of the per-token kernels of the verify forward
+// (embedding, RMSNorm, q/k-norm + RoPE + KV append, split-KV GQA attention) and the
+// step kernels (n-gram proposer, acceptance, commit).
+#pragma once
+#include "mc_common.hpp"
+
+namespace mc {
+
+// Verify-forward token slots.  Slot m carries token slot_tok[m] of row slot_row[m]
+// (-1 = padding) at absolute position slot_pos[m].  Per row, the queries occupy
+// slots [row_slot0[r], row_slot0[r] + n_valid[r]) at positions qbase[r] + j.
+struct SlotView {
+  const int32_t* slot_tok;
+  const int32_t* slot_row;
+  const int32_t* slot_pos;
+  const int32_t* row_slot0;
+  const int32_t* n_valid;
+  const int32_t* qbase;
+};
+
+struct KVLayer {
+  uint16_t* k;  // [R][n_kv][cap][d]
+  uint16_t* v;  // [R][n_kv][cap][d]
+  int cap;
+};
+
+int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, hipStream_t st);
+int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, float eps, uint16_t* y, hipStream_t st);
+// qkv [M][(nq + 2 nkv) d] -> q [M][nq d] (normed + rotated), K/V cache append for valid slots
+int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm, const float* rope_cos,
+                          const float* rope_sin, int M, int nq, int nkv, int d, float eps, const int32_t* slot_row,
+                          const int32_t* slot_pos, KVLayer kv, uint16_t* q_out, hipStream_t st);
+// split-KV attention: partials then combine into att [M][nq d]
+struct AttnWork {
+  float* part_o;   // [M][nq][nchunk][d]
+  float* part_ml;  // [M][nq][nchunk][2]
+  int nchunk;      // ceil(cap / ATTN_CHUNK)
+};
+constexpr int ATTN_CHUNK = 64;
+constexpr int ATTN_QTILE = 16;
+int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
+                     int M, const AttnWork& w, uint16_t* att, hipStream_t st);
+
+int launch_fake_logits(int arch, const int32_t* slot_tok, int M, int V, uint16_t* logits, hipStream_t st);
+
+// Fill positions [0, n) of a row with seeded synthetic bf16 K/V (matches the oracle).
+int launch_kv_synth(KVLayer kv, int layer, int row, int nkv, int d, int n, uint64_t seed, hipStream_t st);
+
+}  // namespace mc

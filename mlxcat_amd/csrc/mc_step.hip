@@ -1,0 +1,500 @@
+// mc_step.hip -- the speculative step's control kernels for gfx950.
+//
+//   propose:  the n-gram proposer of ContinuousBatchGenerator.proposeSuffixTokens
+//             (Sources/MLXCat/TrackB/BatchGenerator.swift:982-1010) for every row at
+//             once, plus the step gate (canSpeculate :957-975, proposal limit :876-884)
+//             and the verify-token layout (:897-898).  The sequential search "longest
+//             suffix first, then the latest earlier non-overlapping occurrence" is the
+//             lexicographic maximum of (min(l(e), n - e), e) over candidate ends e, where
+//             l(e) is the backward match length at e; one block computes every l(e) in
+//             parallel and max-reduces the packed key.
+//   scan:     per (row, verify position): greedy argmax (lowest index on ties), or the
+//             integer-mass target distribution of a sampled row (top-p as
+//             Sampling.swift:847-858 on T=1 masses, then temperature), the accept test
+//             of the draft token (u < p(x), one-hot n-gram draft) and the residual /
+//             bonus sample.
+//   commit:   per row: the acceptance rule (the reference's all-or-nothing loop
+//             :906-947, or longest-prefix / speculative sampling), KV rollback by length,
+//             history append (:1012-1014), stats (:894-895,938,952) and finish reasons
+//             (Scheduler.swift:372-401).
+#include "mc_step.hpp"
+
+namespace mc {
+
+__device__ inline uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// ---------------------------------------------------------------------------
+// n-gram search over one history (block of 256 threads); returns e* or -1
+// ---------------------------------------------------------------------------
+__device__ int ngram_best_end(const int32_t* ctx, int n, int max_suffix, int min_ctx, uint64_t* red) {
+  const int tid = threadIdx.x;
+  if (n < min_ctx) return -1;
+  const int maxlen = min(max_suffix, n - 1);
+  if (maxlen <= 0) return -1;
+  uint64_t best = 0;
+  for (int e = 1 + tid; e <= n - 1; e += blockDim.x) {
+    const int lim = min(maxlen, min(e, n - e));
+    int l = 0;
+    while (l < lim && ctx[e - 1 - l] == ctx[n - 1 - l]) ++l;
+    if (l > 0) best = umax64(best, ((uint64_t)l << 32) | (uint64_t)e);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) best = umax64(best, (uint64_t)__shfl_xor((unsigned long long)best, o));
+  if ((tid & 63) == 0) red[tid >> 6] = best;
+  __syncthreads();
+  uint64_t b = 0;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) b = umax64(b, red[w]);
+  __syncthreads();
+  return b ? (int)(b & 0xFFFFFFFFu) : -1;
+}
+
+__global__ void __launch_bounds__(256) propose_kernel(StepState s) {
+  __shared__ uint64_t red[8];
+  __shared__ int s_nactive;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  if (tid == 0) {
+    int na = 0;
+    for (int i = 0; i < s.R; ++i) na += s.active[i] != 0;
+    s_nactive = na;
+  }
+  __syncthreads();
+  int P = 0;
+  const bool act = s.active[r] != 0;
+  const int32_t* ctx = s.hist + (size_t)r * s.hcap;
+  if (act && s.enabled && s.K > 0 && (!s.single_row_only || s_nactive == 1) && s.hist_len[r] >= s.min_ctx &&
+      (!s.greedy_only || (s.temp[r] == 0.0f && !s.has_seed[r]))) {
+    const int remaining = max(0, s.max_gen[r] - s.gen[r]);
+    if (remaining > 1) {
+      const int limit = min(s.K, remaining - 1);
+      const int n = s.hist_len[r];
+      if (limit > 0) {
+        const int e = ngram_best_end(ctx, n, s.max_suffix, s.min_ctx, red);
+        if (e > 0) P = min(limit, n - e);
+        if (P > 0 && tid < P) s.drafts[r * s.K1 + tid] = ctx[e + tid];
+      }
+    }
+  }
+  if (tid == 0) {
+    s.nprop[r] = act ? P : 0;
+    s.n_valid[r] = act ? P + 1 : 0;
+    s.row_slot0[r] = r * s.K1;
+    s.qbase[r] = s.kv_len[r];
+  }
+  __syncthreads();
+  for (int j = tid; j < s.K1; j += blockDim.x) {
+    const int slot = r * s.K1 + j;
+    if (act && j <= P) {
+      s.slot_tok[slot] = j == 0 ? s.cur[r] : s.drafts[r * s.K1 + j - 1];
+      s.slot_row[slot] = r;
+      s.slot_pos[slot] = s.kv_len[r] + j;
+    } else {
+      s.slot_tok[slot] = 0;
+      s.slot_row[slot] = -1;
+      s.slot_pos[slot] = 0;
+    }
+  }
+}
+
+int launch_propose(const StepState& s, hipStream_t st) {
+  if (s.K1 > 256) return fail(MC_E_INVALID, "propose: K too large");
+  hipLaunchKernelGGL(propose_kernel, dim3(s.R), dim3(256), 0, st, s);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+__global__ void __launch_bounds__(256) ngram_standalone_kernel(const int32_t* hist, const int64_t* off, int max_suffix,
+                                                               int min_ctx, const int32_t* limit, int out_stride,
+                                                               int32_t* out, int32_t* out_len) {
+  __shared__ uint64_t red[8];
+  const int r = blockIdx.x;
+  const int32_t* ctx = hist + off[r];
+  const int n = (int)(off[r + 1] - off[r]);
+  int P = 0;
+  const int lim = limit[r];
+  int e = -1;
+  if (lim > 0) {
+    e = ngram_best_end(ctx, n, max_suffix, min_ctx, red);
+    if (e > 0) P = min(lim, n - e);
+  }
+  for (int j = threadIdx.x; j < P; j += blockDim.x) out[(size_t)r * out_stride + j] = ctx[e + j];
+  if (threadIdx.x == 0) out_len[r] = P;
+}
+
+int launch_ngram_standalone(const int32_t* hist, const int64_t* off, int B, int max_suffix, int min_ctx,
+                            const int32_t* limit, int out_stride, int32_t* out, int32_t* out_len, hipStream_t st) {
+  hipLaunchKernelGGL(ngram_standalone_kernel, dim3(B), dim3(256), 0, st, hist, off, max_suffix, min_ctx, limit,
+                     out_stride, out, out_len);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// acceptance scan
+// ---------------------------------------------------------------------------
+constexpr int SCAN_THREADS = 1024;
+
+__device__ inline float canon_bf16(uint16_t h) { return (h & 0x7FFFu) == 0 ? 0.0f : bf16_to_f32(h); }
+// order-preserving 16-bit key of a bf16 value (with -0 folded into +0)
+__device__ inline uint32_t key16(uint16_t h) {
+  if ((h & 0x7FFFu) == 0) h = 0;
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xFFFFu) : (uint32_t)(h | 0x8000u);
+}
+// floor(u * T / 2^32) for u < 2^32, T < 2^60
+__device__ inline uint64_t mulhi32(uint32_t u, uint64_t T) {
+  const uint64_t lo = (T & 0xFFFFFFFFull) * (uint64_t)u;
+  const uint64_t hi = (T >> 32) * (uint64_t)u;
+  return hi + (lo >> 32);
+}
+
+__device__ inline uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint64_t)__shfl_xor((unsigned long long)v, o);
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  uint64_t t = 0;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+__device__ inline float block_max_f(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  float t = -INFINITY;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = fmaxf(t, red[w]);
+  __syncthreads();
+  return t;
+}
+
+// argmax with the lowest index on ties
+__device__ int block_argmax(const uint16_t* lg, int V, float* redv, int* redi) {
+  const int tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int i = tid; i < V; i += blockDim.x) {
+    const float v = bf16_to_f32(lg[i]);
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  __syncthreads();
+  if ((tid & 63) == 0) { redv[tid >> 6] = bv; redi[tid >> 6] = bi; }
+  __syncthreads();
+  float v = -INFINITY;
+  int idx = 0x7FFFFFFF;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w)
+    if (redv[w] > v || (redv[w] == v && redi[w] < idx)) { v = redv[w]; idx = redi[w]; }
+  __syncthreads();
+  return idx == 0x7FFFFFFF ? 0 : idx;
+}
+
+struct DistDev {
+  float m;          // max logit
+  uint32_t kstar;   // smallest kept key (0 = all kept)
+  uint64_t total;   // kept temperature mass
+};
+
+__device__ inline uint64_t tmass(const DistDev& d, uint16_t h, float inv_t) {
+#pragma clang fp contract(off)
+  if (key16(h) < d.kstar) return 0;
+  const float v = canon_bf16(h);
+  return mass_of(exp_neg_det((v - d.m) * inv_t));
+}
+
+__device__ DistDev dist_build_dev(const uint16_t* lg, int V, float inv_t, float top_p, uint64_t* hist, uint64_t* red,
+                                  float* redf, int* s_int, uint64_t* s_u64) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  DistDev d;
+  float mx = -INFINITY;
+  for (int i = tid; i < V; i += blockDim.x) mx = fmaxf(mx, canon_bf16(lg[i]));
+  d.m = block_max_f(mx, redf);
+  d.kstar = 0;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    for (int i = tid; i < 512; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    uint64_t t1 = 0;
+    for (int i = tid; i < V; i += blockDim.x) {
+      const uint16_t h = lg[i];
+      const uint64_t w = mass_of(exp_neg_det(canon_bf16(h) - d.m));
+      t1 += w;
+      if (w) atomicAdd((unsigned long long*)&hist[key16(h) >> 8], (unsigned long long)w);
+    }
+    const uint64_t total1 = block_sum_u64(t1, red);
+    const double X = (double)top_p * (double)total1;
+    if (tid == 0) {
+      uint64_t cum = 0, base = 0;
+      int hb = -1;
+      for (int b = 255; b >= 0; --b) {
+        if (hist[b] == 0) continue;
+        if (!((double)cum < X)) break;
+        hb = b;
+        base = cum;
+        cum += hist[b];
+      }
+      s_int[0] = hb;
+      s_u64[0] = base;
+    }
+    __syncthreads();
+    const int hb = s_int[0];
+    for (int i = tid; i < V; i += blockDim.x) {
+      const uint16_t h = lg[i];
+      const uint32_t k = key16(h);
+      if ((int)(k >> 8) != hb) continue;
+      const uint64_t w = mass_of(exp_neg_det(canon_bf16(h) - d.m));
+      if (w) atomicAdd((unsigned long long*)&hist[256 + (k & 255u)], (unsigned long long)w);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t cum = s_u64[0];
+      int lo = -1;
+      for (int b = 255; b >= 0; --b) {
+        if (hist[256 + b] == 0) continue;
+        if (!((double)cum < X)) break;
+        lo = b;
+        cum += hist[256 + b];
+      }
+      // hb >= 0 and lo >= 0 whenever the row has a finite maximum
+      s_int[1] = (hb < 0 || lo < 0) ? 0 : ((hb << 8) | lo);
+    }
+    __syncthreads();
+    d.kstar = (uint32_t)s_int[1];
+  }
+  uint64_t tt = 0;
+  for (int i = tid; i < V; i += blockDim.x) tt += tmass(d, lg[i], inv_t);
+  d.total = block_sum_u64(tt, red);
+  return d;
+}
+
+// index-order inverse-CDF sample of floor(u * total' / 2^32), total' excluding `ex`
+__device__ int dist_sample_dev(const DistDev& d, const uint16_t* lg, int V, float inv_t, uint32_t u, int ex,
+                               uint64_t wx, uint64_t* scan, int* s_int) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const uint64_t total = d.total - (ex >= 0 ? wx : 0);
+  const uint64_t R = mulhi32(u, total);
+  const int chunk = (V + nt - 1) / nt;
+  const int b0 = tid * chunk, b1 = min(V, b0 + chunk);
+  uint64_t cs = 0;
+  for (int i = b0; i < b1; ++i)
+    if (i != ex) cs += tmass(d, lg[i], inv_t);
+  scan[tid] = cs;
+  if (tid == 0) s_int[2] = -1;
+  __syncthreads();
+  // exclusive prefix over threads (sequential per wave leader; 16 waves)
+  if (tid == 0) {
+    uint64_t acc = 0;
+    for (int i = 0; i < nt; ++i) {
+      const uint64_t v = scan[i];
+      scan[i] = acc;
+      acc += v;
+    }
+  }
+  __syncthreads();
+  const uint64_t start = scan[tid];
+  if (R >= start && R < start + cs) {
+    uint64_t c = start;
+    for (int i = b0; i < b1; ++i) {
+      if (i == ex) continue;
+      const uint64_t w = tmass(d, lg[i], inv_t);
+      if (w == 0) continue;
+      if (c + w > R) { s_int[2] = i; break; }
+      c += w;
+    }
+  }
+  __syncthreads();
+  const int tok = s_int[2];
+  __syncthreads();
+  return tok < 0 ? 0 : tok;
+}
+
+__global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, const uint16_t* logits, int row_filter) {
+  __shared__ uint64_t hist[512];
+  __shared__ uint64_t scan[SCAN_THREADS];
+  __shared__ uint64_t red[16];
+  __shared__ float redf[16];
+  __shared__ int redi[16];
+  __shared__ int s_int[4];
+  __shared__ uint64_t s_u64[2];
+  const int r = blockIdx.x, j = blockIdx.y;
+  if (row_filter >= 0 && r != row_filter) return;
+  if (!s.active[r] || j >= s.n_valid[r]) return;
+  const int P = s.nprop[r];
+  const int slot = s.row_slot0[r] + j;
+  const uint16_t* lg = logits + (size_t)slot * s.V;
+  const int V = s.V;
+  if (s.temp[r] == 0.0f) {
+    const int t = block_argmax(lg, V, redf, redi);
+    if (threadIdx.x == 0) s.scan_tok[r * s.K1 + j] = t;
+    return;
+  }
+  const float inv_t = s.inv_temp[r];
+  const DistDev d = dist_build_dev(lg, V, inv_t, s.top_p[r], hist, red, redf, s_int, s_u64);
+  const uint64_t seed = s.seed[r], ctr = s.counter[r];
+  if (j < P) {
+    const int x = s.drafts[r * s.K1 + j];
+    const uint64_t wx = tmass(d, lg[x], inv_t);
+    const uint32_t u0 = uniform_u32(seed, ctr, (uint32_t)j, 0u);
+    const int acc = mulhi32(u0, d.total) < wx;
+    const int res = dist_sample_dev(d, lg, V, inv_t, uniform_u32(seed, ctr, (uint32_t)j, 1u), x, wx, scan, s_int);
+    if (threadIdx.x == 0) {
+      s.scan_acc[r * s.K1 + j] = acc;
+      s.scan_res[r * s.K1 + j] = res;
+    }
+  } else {
+    const int res = dist_sample_dev(d, lg, V, inv_t, uniform_u32(seed, ctr, (uint32_t)j, 1u), -1, 0, scan, s_int);
+    if (threadIdx.x == 0) s.scan_res[r * s.K1 + j] = res;
+  }
+}
+
+int launch_accept_scan(const StepState& s, const uint16_t* logits, int row_filter, hipStream_t st) {
+  hipLaunchKernelGGL(accept_scan_kernel, dim3(s.R, s.K1), dim3(SCAN_THREADS), 0, st, s, logits, row_filter);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// commit: one thread per row
+// ---------------------------------------------------------------------------
+__device__ inline bool is_eos(const StepState& s, int r, int tok) {
+  const int n = s.n_eos[r];
+  for (int i = 0; i < n; ++i)
+    if (s.eos[r * 8 + i] == tok) return true;
+  return false;
+}
+
+// Acceptance decision of one row.  Writes the emitted tokens to `out`, returns their
+// count; *keep = verified positions kept in the KV (current token + accepted drafts),
+// *nacc = drafts accepted, *rejected = 1 when a proposal was (partly) rejected.
+__device__ int decide_row(const StepState& s, int r, int32_t* out, int* keep, int* nacc, int* rejected) {
+  const int P = s.nprop[r], K1 = s.K1;
+  const int32_t* dr = s.drafts + r * K1;
+  const int32_t* st = s.scan_tok + r * K1;
+  const int32_t* sa = s.scan_acc + r * K1;
+  const int32_t* sr = s.scan_res + r * K1;
+  const bool greedy = s.temp[r] == 0.0f;
+  const int rej = s.reject[r];
+  int n = 0;
+  *keep = 1;
+  *nacc = 0;
+  *rejected = 0;
+  if (greedy && s.acceptance == MC_ACCEPT_ALL_OR_NOTHING) {
+    if (P == 0) {
+      out[n++] = st[0];
+    } else {
+      bool all = true;
+      int na = 0;
+      for (int pos = 0; pos <= P; ++pos) {
+        const int t = st[pos];
+        if (rej >= 0 && t == rej) { all = false; break; }        // :920-923
+        if (pos < P && t != dr[pos]) { all = false; break; }    // :925-928
+        out[na++] = t;
+        if (is_eos(s, r, t)) break;                             // :932-934
+      }
+      if (!all) {
+        *rejected = 1;                                          // :938
+        out[0] = st[0];                                         // :939 one-token decode == position 0
+        n = 1;
+      } else {
+        n = na;
+        *keep = P + 1;                                          // :942 adopt the verified positions
+        *nacc = na > 1 ? na - 1 : 0;                            // :952
+      }
+    }
+  } else {
+    int cap = P;
+    const int f = s.forced ? s.forced[r] : -1;
+    if (f >= 0 && f < cap) cap = f;
+    int a = 0;
+    bool stop = false;
+    for (int pos = 0; pos < P; ++pos) {
+      int t;
+      if (greedy) {
+        t = st[pos];
+        if (pos >= cap || t != dr[pos] || t == rej) { out[n++] = t; stop = true; break; }
+      } else {
+        if (!(pos < cap && sa[pos])) { out[n++] = sr[pos]; stop = true; break; }
+        t = dr[pos];
+      }
+      out[n++] = t;
+      ++a;
+      if (t == rej || is_eos(s, r, t)) { stop = true; break; }
+    }
+    if (!stop) out[n++] = greedy ? st[P] : sr[P];
+    *keep = a + 1;
+    *nacc = a;
+    *rejected = (P > 0 && a < P) ? 1 : 0;
+  }
+  return n;
+}
+
+__global__ void commit_kernel(StepState s, int row_filter) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= s.R) return;
+  if (row_filter >= 0 && r != row_filter) return;
+  if (!s.active[r]) {
+    s.out_cnt[r] = 0;
+    s.out_fin[r] = 0;
+    return;
+  }
+  const int P = s.nprop[r];
+  int32_t* out = s.out_tok + r * s.K1;
+  int keep, nacc, rejected;
+  const int n = decide_row(s, r, out, &keep, &nacc, &rejected);
+  if (P > 0) {
+    atomicAdd(&s.stats[0], (unsigned long long)P);        // :895
+    atomicAdd(&s.stats[1], (unsigned long long)nacc);     // :952
+    atomicAdd(&s.stats[2], 1ull);                         // :894
+    atomicAdd(&s.stats[3], (unsigned long long)rejected); // :938
+  }
+  s.counter[r] += 1;
+  s.kv_len[r] = s.qbase[r] + keep;  // rollback: keep current token + accepted drafts
+  int fin = 0, emitted = 0;
+  int32_t* h = s.hist + (size_t)r * s.hcap;
+  for (int z = 0; z < n; ++z) {
+    const int t = out[z];
+    if (s.hist_len[r] < s.hcap) h[s.hist_len[r]++] = t;
+    s.gen[r] += 1;
+    ++emitted;
+    fin = is_eos(s, r, t) ? 1 : (s.gen[r] >= s.max_gen[r] ? 2 : 0);
+    if (fin) break;
+  }
+  s.cur[r] = out[n - 1];
+  s.out_cnt[r] = emitted;
+  s.out_fin[r] = fin;
+  if (fin) s.active[r] = 0;
+}
+
+// decision only (mc_accept): no state update
+__global__ void decide_kernel(StepState s, int32_t* n_emit, int32_t* keep_out, int32_t* nacc_out) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= s.R) return;
+  int keep, nacc, rejected;
+  const int n = decide_row(s, r, s.out_tok + r * s.K1, &keep, &nacc, &rejected);
+  n_emit[r] = n;
+  keep_out[r] = keep;
+  nacc_out[r] = nacc;
+}
+
+int launch_decide(const StepState& s, int32_t* n_emit, int32_t* keep_out, int32_t* nacc_out, hipStream_t st) {
+  hipLaunchKernelGGL(decide_kernel, dim3((s.R + 63) / 64), dim3(64), 0, st, s, n_emit, keep_out, nacc_out);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+int launch_commit(const StepState& s, int row_filter, hipStream_t st) {
+  hipLaunchKernelGGL(commit_kernel, dim3((s.R + 63) / 64), dim3(64), 0, st, s, row_filter);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+}  // namespace mc

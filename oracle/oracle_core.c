@@ -1,0 +1,572 @@
+/*
+ * oracle.c -- CPU restatement of mlxcat's n-gram speculative-decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and CPU baseline for the HIP
+ * product.  The product never links or calls this file.  Reference citations
+ * are to local-ai-cat/mlxcat (paths relative to its root); see oracle.h.
+ *
+ * Built with -ffp-contract=off so that the integer-mass acceptance helpers
+ * (or_exp_neg and the top-p / sampling arithmetic) evaluate exactly the
+ * operation sequence the GPU evaluates.
+ */
+#include "oracle.h"
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ */
+/* integer generators                                                   */
+/* ------------------------------------------------------------------ */
+uint64_t or_mix64(uint64_t z) {
+  /* splitmix64 finalizer (Steele, Lea, Flood 2014) */
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint32_t or_uniform_u32(uint64_t seed, uint64_t counter, uint32_t pos, uint32_t kind) {
+  uint64_t h = or_mix64(seed ^ 0x5851F42D4C957F2Dull);
+  h = or_mix64(h ^ counter);
+  h = or_mix64(h ^ (((uint64_t)pos << 8) | kind));
+  return (uint32_t)(h >> 32);
+}
+
+uint16_t or_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t r = u + 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(r >> 16);
+}
+
+float or_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline float bf(uint16_t h) { return or_bf16_to_f32(h); }
+static inline uint16_t tobf(float f) { return or_f32_to_bf16(f); }
+
+uint64_t or_tensor_id(int layer, int which) { return ((uint64_t)(layer + 1) << 8) | (uint64_t)which; }
+uint64_t or_expert_tensor_id(int layer, int expert, int which) {
+  return 0x100000000ull | ((uint64_t)layer << 20) | ((uint64_t)expert << 4) | (uint64_t)which;
+}
+
+void or_gen_linear(uint64_t seed, uint64_t tid, int N, int K, int scale_exp, uint32_t* wq,
+                   uint16_t* scales, uint16_t* biases) {
+  const int KW = K / 8, G = K / 64;
+  const uint64_t base = or_mix64(seed ^ or_mix64(tid));
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n) {
+    for (int kw = 0; kw < KW; ++kw) {
+      uint64_t idx = ((uint64_t)n * (uint64_t)KW + (uint64_t)kw) * 2u;
+      uint64_t h0 = or_mix64(base ^ idx), h1 = or_mix64(base ^ (idx + 1));
+      uint32_t w = 0;
+      for (int j = 0; j < 8; ++j) {
+        uint64_t h = j < 4 ? h0 : h1;
+        uint32_t q = (uint32_t)__builtin_popcountll((h >> (15 * (j & 3))) & 0x7FFFull);
+        w |= q << (4 * j);
+      }
+      wq[(size_t)n * KW + kw] = w;
+    }
+    for (int g = 0; g < G; ++g) {
+      uint64_t h = or_mix64(base ^ 0xA5A5A5A500000000ull ^ ((uint64_t)n * (uint64_t)G + (uint64_t)g));
+      uint16_t sb = (uint16_t)(((uint32_t)(127 + scale_exp) << 7) | (0x28u + (uint32_t)(h & 0xFu)));
+      float s = bf(sb);
+      scales[(size_t)n * G + g] = sb;
+      biases[(size_t)n * G + g] = tobf(-7.5f * s);
+    }
+  }
+}
+
+void or_gen_norm(uint64_t seed, uint64_t tid, int n, uint16_t* w) {
+  const uint64_t base = or_mix64(seed ^ or_mix64(tid ^ 0x4E4F524Dull));
+  for (int i = 0; i < n; ++i) {
+    uint64_t h = or_mix64(base ^ (uint64_t)i);
+    int k = (int)(h % 32u) - 16;
+    w[i] = tobf(1.0f + (float)k / 128.0f);
+  }
+}
+
+/* ------------------------------------------------------------------ */
+/* exp for the acceptance masses                                        */
+/* ------------------------------------------------------------------ */
+float or_exp_neg(float x) {
+  /* x <= 0.  2^y with y = x*log2(e); y = n + f, n = rint(y), |f| <= 1/2;
+   * 2^f = sum_k (f ln2)^k / k!, k <= 7, coefficients (ln 2)^k / k! rounded to float. */
+  if (!(x > -87.0f)) return 0.0f;
+  const float LOG2E = 1.44269504088896341f;
+  float y = x * LOG2E;
+  float n = rintf(y);
+  float f = y - n;
+  if (n < -40.0f) return 0.0f;
+  const float c7 = 1.52527338e-05f, c6 = 1.54035304e-04f, c5 = 1.33335581e-03f,
+              c4 = 9.61812911e-03f, c3 = 5.55041087e-02f, c2 = 2.40226507e-01f,
+              c1 = 6.93147181e-01f, c0 = 1.0f;
+  float p = c7;
+  p = fmaf(p, f, c6);
+  p = fmaf(p, f, c5);
+  p = fmaf(p, f, c4);
+  p = fmaf(p, f, c3);
+  p = fmaf(p, f, c2);
+  p = fmaf(p, f, c1);
+  p = fmaf(p, f, c0);
+  return ldexpf(p, (int)n);
+}
+
+static inline uint64_t mass_of(float e) { return (uint64_t)rintf(e * 4294967296.0f); }
+
+/* ------------------------------------------------------------------ */
+/* n-gram proposer: restates BatchGenerator.swift:982-1010              */
+/* ------------------------------------------------------------------ */
+int or_ngram_propose(const int32_t* ctx, int n, int max_suffix, int min_context, int limit,
+                     int32_t* out) {
+  if (n < min_context || limit <= 0) return 0;                 /* :983 */
+  int max_len = max_suffix < n - 1 ? max_suffix : n - 1;       /* :987-990 */
+  if (max_len <= 0) return 0;                                  /* :991 */
+  for (int L = max_len; L >= 1; --L) {                         /* :993 */
+    int suffix_start = n - L;                                  /* :994 */
+    if (suffix_start <= 0) continue;                           /* :996 */
+    for (int c = suffix_start - 1; c >= 0; --c) {              /* :998 */
+      int cend = c + L;                                        /* :999 */
+      if (cend > suffix_start) continue;                       /* :1000 */
+      if (memcmp(ctx + c, ctx + suffix_start, (size_t)L * sizeof(int32_t)) == 0) {  /* :1001 */
+        int ps = cend;                                         /* :1002 */
+        int pe = n < ps + limit ? n : ps + limit;              /* :1003 */
+        if (ps >= pe) continue;                                /* :1004 */
+        for (int i = ps; i < pe; ++i) out[i - ps] = ctx[i];
+        return pe - ps;                                        /* :1005 */
+      }
+    }
+  }
+  return 0;                                                    /* :1009 */
+}
+
+/* ------------------------------------------------------------------ */
+/* acceptance building blocks                                           */
+/* ------------------------------------------------------------------ */
+int or_argmax_bf16(const uint16_t* logits, int V) {
+  int best = 0;
+  float bv = bf(logits[0]);
+  for (int i = 1; i < V; ++i) {
+    float v = bf(logits[i]);
+    if (v > bv) { bv = v; best = i; }
+  }
+  return best;
+}
+
+static inline float canon(uint16_t h) {  /* -0 -> +0 */
+  float v = bf(h);
+  return v == 0.0f ? 0.0f : v;
+}
+
+typedef struct { float v; uint64_t w; } vw_t;
+static int cmp_desc(const void* a, const void* b) {
+  float x = ((const vw_t*)a)->v, y = ((const vw_t*)b)->v;
+  return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+void or_dist_build(const uint16_t* logits, int V, float temperature, float top_p, or_dist* d) {
+  float m = -INFINITY;
+  for (int i = 0; i < V; ++i) { float v = canon(logits[i]); if (v > m) m = v; }
+  d->max_logit = m;
+  d->filtered = (top_p > 0.0f && top_p < 1.0f);
+  d->tau = -INFINITY;
+  if (d->filtered) {
+    /* Sampling.swift:847-858: drop sorted positions whose mass strictly above is
+     * >= topP * total; keep every token whose logit is >= the first kept value. */
+    vw_t* a = (vw_t*)malloc(sizeof(vw_t) * (size_t)V);
+    uint64_t total1 = 0;
+    for (int i = 0; i < V; ++i) {
+      a[i].v = canon(logits[i]);
+      a[i].w = mass_of(or_exp_neg(a[i].v - m));
+      total1 += a[i].w;
+    }
+    qsort(a, (size_t)V, sizeof(vw_t), cmp_desc);
+    double X = (double)top_p * (double)total1;
+    uint64_t above = 0;
+    int i = 0;
+    while (i < V) {
+      float v = a[i].v;
+      if (!((double)above < X)) break;
+      d->tau = v;
+      while (i < V && a[i].v == v) { above += a[i].w; ++i; }
+    }
+    free(a);
+  }
+  float inv_t = 1.0f / temperature;
+  uint64_t tot = 0;
+  for (int i = 0; i < V; ++i) {
+    float v = canon(logits[i]);
+    if (d->filtered && v < d->tau) continue;
+    tot += mass_of(or_exp_neg((v - m) * inv_t));
+  }
+  d->total = tot;
+}
+
+uint64_t or_dist_mass(const or_dist* d, const uint16_t* logits, float inv_temp, int token) {
+  float v = canon(logits[token]);
+  if (d->filtered && v < d->tau) return 0;
+  return mass_of(or_exp_neg((v - d->max_logit) * inv_temp));
+}
+
+int or_dist_sample(const or_dist* d, const uint16_t* logits, int V, float inv_temp, uint32_t u,
+                   int exclude) {
+  uint64_t total = d->total;
+  if (exclude >= 0) total -= or_dist_mass(d, logits, inv_temp, exclude);
+  unsigned __int128 prod = (unsigned __int128)u * (unsigned __int128)total;
+  uint64_t R = (uint64_t)(prod >> 32);
+  uint64_t c = 0;
+  int last = -1;
+  for (int i = 0; i < V; ++i) {
+    if (i == exclude) continue;
+    uint64_t w = or_dist_mass(d, logits, inv_temp, i);
+    if (w == 0) continue;
+    last = i;
+    if (c + w > R) return i;
+    c += w;
+  }
+  return last; /* unreachable when total > 0 */
+}
+
+static int accept_draft(const or_dist* d, const uint16_t* logits, float inv_temp, int x, uint32_t u) {
+  uint64_t w = or_dist_mass(d, logits, inv_temp, x);
+  unsigned __int128 lhs = (unsigned __int128)u * (unsigned __int128)d->total;
+  unsigned __int128 rhs = (unsigned __int128)w << 32;
+  return lhs < rhs;
+}
+
+/* ------------------------------------------------------------------ */
+/* KV trim known answer: BatchCache.swift:403-424                       */
+/* ------------------------------------------------------------------ */
+int or_batch_trim(int* idx, int B, int32_t* lp, int32_t* off, int n) {
+  int trimmed = *idx < n ? *idx : n;                                       /* :406 */
+  if (trimmed <= 0) return 0;                                              /* :407 */
+  int cur = *idx;
+  int* row_tr = (int*)malloc(sizeof(int) * (size_t)(B > 0 ? B : 1));
+  for (int r = 0; r < B; ++r) {                                            /* :412-414 */
+    int avail = cur - lp[r];
+    if (avail < 0) avail = 0;
+    row_tr[r] = trimmed < avail ? trimmed : avail;
+  }
+  *idx -= trimmed;                                                         /* :416 */
+  for (int r = 0; r < B; ++r) {
+    int rem = cur - lp[r] - row_tr[r];                                     /* :418 */
+    if (rem < 0) rem = 0;
+    lp[r] = *idx - rem;                                                    /* :419 */
+    off[r] -= row_tr[r];                                                   /* :422 */
+  }
+  free(row_tr);
+  return trimmed;
+}
+
+/* ------------------------------------------------------------------ */
+/* generator + scheduler restatement                                    */
+/* ------------------------------------------------------------------ */
+typedef struct or_row {
+  int active;
+  int32_t* hist;      /* speculativeTokenHistory: prompt + generated (incl. pending current) */
+  int hist_len;
+  int generated;      /* generatedTokenHistory.count */
+  int max_tokens;
+  int cur;            /* currentTokens[row], not yet in the KV */
+  or_sampling sp;
+  uint64_t seed;
+  uint64_t counter;   /* per-row draw counter */
+} or_row;
+
+struct or_generator {
+  or_model* m;
+  or_spec_config cfg;
+  int max_rows, max_hist;
+  or_row* rows;
+  or_stats stats;
+  uint64_t global_seed;
+  uint64_t unseeded_count;
+  int32_t* widths;
+  int n_widths, cap_widths;
+};
+
+or_generator* or_generator_create(or_model* m, const or_spec_config* cfg, int max_rows,
+                                  int max_hist, uint64_t global_seed) {
+  or_generator* g = (or_generator*)calloc(1, sizeof(or_generator));
+  g->m = m;
+  g->cfg = *cfg;
+  /* SpeculativeDecodingConfiguration clamps, BatchGenerator.swift:23-25 */
+  if (g->cfg.max_proposal_tokens < 0) g->cfg.max_proposal_tokens = 0;
+  if (g->cfg.max_suffix_tokens < 1) g->cfg.max_suffix_tokens = 1;
+  if (g->cfg.min_context_tokens < 2) g->cfg.min_context_tokens = 2;
+  g->max_rows = max_rows;
+  g->max_hist = max_hist;
+  g->global_seed = global_seed;
+  g->rows = (or_row*)calloc((size_t)max_rows, sizeof(or_row));
+  for (int r = 0; r < max_rows; ++r) g->rows[r].hist = (int32_t*)malloc(sizeof(int32_t) * (size_t)max_hist);
+  g->cap_widths = 4096;
+  g->widths = (int32_t*)malloc(sizeof(int32_t) * (size_t)g->cap_widths);
+  return g;
+}
+
+void or_generator_destroy(or_generator* g) {
+  if (!g) return;
+  for (int r = 0; r < g->max_rows; ++r) free(g->rows[r].hist);
+  free(g->rows);
+  free(g->widths);
+  free(g);
+}
+
+static void record_width(or_generator* g, int w) {
+  if (g->n_widths < g->cap_widths) g->widths[g->n_widths++] = w;
+}
+
+static int is_eos(const or_sampling* sp, int tok) {
+  for (int i = 0; i < sp->n_eos; ++i)
+    if (sp->eos[i] == tok) return 1;
+  return 0;
+}
+
+/* sample one position: greedy argmax at T == 0, else integer-mass sampling */
+static int sample_pos(const or_row* rw, const uint16_t* lg, int V, uint32_t u) {
+  if (rw->sp.temperature == 0.0f) return or_argmax_bf16(lg, V);
+  or_dist d;
+  or_dist_build(lg, V, rw->sp.temperature, rw->sp.top_p, &d);
+  return or_dist_sample(&d, lg, V, 1.0f / rw->sp.temperature, u, -1);
+}
+
+static int finish_of(const or_row* rw, int tok) {   /* Scheduler.swift:1215-1227 */
+  if (is_eos(&rw->sp, tok)) return 1;
+  if (rw->generated >= rw->max_tokens) return 2;
+  return 0;
+}
+
+int or_generator_insert(or_generator* g, int row, const int32_t* prompt, int n_prompt,
+                        int max_tokens, const or_sampling* sp, int* finished) {
+  if (row < 0 || row >= g->max_rows || n_prompt < 1 || n_prompt + 2 > g->max_hist) return -1;
+  or_row* rw = &g->rows[row];
+  const int V = or_model_cfg(g->m)->vocab;
+  or_kv_set_len(g->m, row, 0);
+  /* prefill all but the last prompt token, then the last one alone (Scheduler.swift:722-739) */
+  if (n_prompt > 1) {
+    int cnt = n_prompt - 1;
+    if (or_forward(g->m, 1, &row, &cnt, prompt, NULL)) return -2;
+  }
+  uint16_t* lg = (uint16_t*)malloc(2 * (size_t)V);
+  int one = 1;
+  if (or_kv_len(g->m, row) > 0) record_width(g, 1);
+  if (or_forward(g->m, 1, &row, &one, prompt + n_prompt - 1, lg)) { free(lg); return -2; }
+  rw->sp = *sp;
+  rw->seed = sp->has_seed ? sp->seed : or_mix64(g->global_seed ^ or_mix64(++g->unseeded_count));
+  rw->counter = 0;
+  int tok = sample_pos(rw, lg, V, or_uniform_u32(rw->seed, rw->counter, 0, 1));
+  rw->counter++;
+  free(lg);
+  rw->generated = 1;
+  rw->max_tokens = max_tokens;
+  memcpy(rw->hist, prompt, sizeof(int32_t) * (size_t)n_prompt);
+  rw->hist[n_prompt] = tok;
+  rw->hist_len = n_prompt + 1;
+  rw->cur = tok;
+  int fin = finish_of(rw, tok);
+  if (finished) *finished = fin;
+  rw->active = fin == 0;
+  return tok;
+}
+
+int or_generator_insert_prefilled(or_generator* g, int row, const int32_t* ctx, int n_ctx,
+                                  int max_tokens, const or_sampling* sp) {
+  if (row < 0 || row >= g->max_rows || n_ctx < 1 || n_ctx > g->max_hist) return -1;
+  if (or_kv_len(g->m, row) != n_ctx - 1) return -3;
+  or_row* rw = &g->rows[row];
+  rw->sp = *sp;
+  rw->seed = sp->has_seed ? sp->seed : or_mix64(g->global_seed ^ or_mix64(++g->unseeded_count));
+  rw->counter = 0;
+  rw->generated = 1;
+  rw->max_tokens = max_tokens;
+  memcpy(rw->hist, ctx, sizeof(int32_t) * (size_t)n_ctx);
+  rw->hist_len = n_ctx;
+  rw->cur = ctx[n_ctx - 1];
+  rw->active = 1;
+  return 0;
+}
+
+void or_generator_remove(or_generator* g, int row) {
+  if (row >= 0 && row < g->max_rows) g->rows[row].active = 0;
+}
+
+/* canSpeculate, BatchGenerator.swift:957-975, generalised to many rows */
+static int can_speculate(const or_generator* g, const or_row* rw, int n_active) {
+  if (!g->cfg.enabled || g->cfg.max_proposal_tokens <= 0) return 0;
+  if (g->cfg.single_row_only && n_active != 1) return 0;
+  if (rw->hist_len < g->cfg.min_context_tokens) return 0;
+  if (g->cfg.greedy_only && (rw->sp.temperature != 0.0f || rw->sp.has_seed)) return 0;
+  return 1;
+}
+
+int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
+                      int32_t* out_finish, const int32_t* forced_accept) {
+  const int K = g->cfg.max_proposal_tokens, V = or_model_cfg(g->m)->vocab, R = g->max_rows;
+  int n_active = 0;
+  for (int r = 0; r < R; ++r) n_active += g->rows[r].active;
+  for (int r = 0; r < R; ++r) { out_counts[r] = 0; out_finish[r] = 0; }
+  if (n_active == 0) return 0;
+  int32_t* rows = (int32_t*)malloc(sizeof(int32_t) * (size_t)R);
+  int32_t* counts = (int32_t*)malloc(sizeof(int32_t) * (size_t)R);
+  int32_t* drafts = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * (size_t)(K + 1));
+  int32_t* nprop = (int32_t*)calloc((size_t)R, sizeof(int32_t));
+  int32_t* toks = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * (size_t)(K + 1));
+  int nr = 0, M = 0;
+  for (int r = 0; r < R; ++r) {
+    or_row* rw = &g->rows[r];
+    if (!rw->active) continue;
+    int P = 0;
+    if (can_speculate(g, rw, n_active)) {
+      int remaining = rw->max_tokens - rw->generated;                        /* :977-980 */
+      if (remaining < 0) remaining = 0;
+      if (remaining > 1) {                                                   /* :878 */
+        int limit = K < remaining - 1 ? K : remaining - 1;                   /* :883 */
+        if (limit > 0)
+          P = or_ngram_propose(rw->hist, rw->hist_len, g->cfg.max_suffix_tokens,
+                               g->cfg.min_context_tokens, limit, drafts + (size_t)r * (K + 1));
+      }
+    }
+    nprop[r] = P;
+    if (P > 0) { g->stats.proposal_batches++; g->stats.proposed += P; }     /* :894-895 */
+    rows[nr] = r;
+    counts[nr] = P + 1;
+    toks[M] = rw->cur;                                                       /* :897 */
+    for (int j = 0; j < P; ++j) toks[M + 1 + j] = drafts[(size_t)r * (K + 1) + j];
+    if (or_kv_len(g->m, r) > 0) record_width(g, P + 1);
+    M += P + 1;
+    nr++;
+  }
+  uint16_t* lg = (uint16_t*)malloc(2 * (size_t)M * (size_t)V);
+  if (or_forward(g->m, nr, rows, counts, toks, lg)) {
+    free(rows); free(counts); free(drafts); free(nprop); free(toks); free(lg);
+    return -1;
+  }
+  int produced = 0;
+  for (int i = 0, t0 = 0; i < nr; t0 += counts[i], ++i) {
+    const int r = rows[i], P = nprop[r];
+    or_row* rw = &g->rows[r];
+    const int32_t* dr = drafts + (size_t)r * (K + 1);
+    int32_t* out = out_tokens + (size_t)r * (K + 1);
+    int n_emit = 0, kv_keep = 1;
+    const int sampled = rw->sp.temperature != 0.0f;
+    const float inv_t = sampled ? 1.0f / rw->sp.temperature : 0.0f;
+    if (!sampled && g->cfg.acceptance == OR_ACCEPT_ALL_OR_NOTHING) {
+      /* BatchGenerator.swift:906-947 */
+      int all = 1, n_acc = 0;
+      int tmp[64];
+      for (int pos = 0; pos <= P; ++pos) {
+        int s = or_argmax_bf16(lg + (size_t)(t0 + pos) * V, V);
+        if (rw->sp.reject_token >= 0 && s == rw->sp.reject_token) { all = 0; break; }  /* :920-923 */
+        if (pos < P && s != dr[pos]) { all = 0; break; }                            /* :925-928 */
+        tmp[n_acc++] = s;
+        if (is_eos(&rw->sp, s)) break;                                              /* :932-934 */
+      }
+      if (P == 0) {
+        out[0] = or_argmax_bf16(lg + (size_t)t0 * V, V);   /* decodeOneToken */
+        n_emit = 1;
+        kv_keep = 1;
+      } else if (!all) {
+        g->stats.rejected_batches++;                                  /* :938 */
+        /* :939 decodeOneToken on the original cache == position 0 of the verify */
+        out[0] = or_argmax_bf16(lg + (size_t)t0 * V, V);
+        n_emit = 1;
+        kv_keep = 1;
+      } else {
+        for (int z = 0; z < n_acc; ++z) out[z] = tmp[z];
+        n_emit = n_acc;
+        kv_keep = P + 1;                                              /* :942 adopt working cache */
+        g->stats.accepted += n_acc - 1 > 0 ? n_acc - 1 : 0;          /* :952 */
+      }
+    } else {
+      /* prefix acceptance (greedy) and speculative sampling (temperature > 0):
+       * accept drafts while they agree, emit the correction (or the bonus token
+       * after a full accept), keep current token + accepted drafts in the KV. */
+      int cap = forced_accept ? forced_accept[r] : P;
+      if (cap > P) cap = P;
+      if (cap < 0) cap = 0;
+      int a = 0, stop = 0;
+      for (int pos = 0; pos < P; ++pos) {
+        const uint16_t* row_lg = lg + (size_t)(t0 + pos) * V;
+        int tok;
+        if (!sampled) {
+          tok = or_argmax_bf16(row_lg, V);
+          if (pos >= cap || tok != dr[pos] || tok == rw->sp.reject_token) {
+            out[n_emit++] = tok;
+            stop = 1;
+            break;
+          }
+        } else {
+          or_dist d;
+          or_dist_build(row_lg, V, rw->sp.temperature, rw->sp.top_p, &d);
+          int ok = pos < cap && accept_draft(&d, row_lg, inv_t, dr[pos],
+                                             or_uniform_u32(rw->seed, rw->counter, (uint32_t)pos, 0));
+          if (!ok) {
+            out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t,
+                                           or_uniform_u32(rw->seed, rw->counter, (uint32_t)pos, 1), dr[pos]);
+            stop = 1;
+            break;
+          }
+          tok = dr[pos];
+        }
+        out[n_emit++] = tok;
+        a++;
+        if (tok == rw->sp.reject_token || is_eos(&rw->sp, tok)) { stop = 1; break; }
+      }
+      if (!stop) {
+        const uint16_t* row_lg = lg + (size_t)(t0 + P) * V;
+        out[n_emit++] = sampled ? sample_pos(rw, row_lg, V, or_uniform_u32(rw->seed, rw->counter, (uint32_t)P, 1))
+                                : or_argmax_bf16(row_lg, V);
+      }
+      kv_keep = a + 1;
+      if (P > 0) {
+        g->stats.accepted += a;
+        if (a < P) g->stats.rejected_batches++;
+      }
+    }
+    rw->counter++;
+    /* rollback: drop verified positions beyond what is kept (O(1): length only) */
+    or_kv_set_len(g->m, r, or_kv_len(g->m, r) - (P + 1 - kv_keep));
+    int fin = 0, emitted = 0;
+    for (int z = 0; z < n_emit; ++z) {
+      const int tok = out[z];
+      if (rw->hist_len < g->max_hist) rw->hist[rw->hist_len++] = tok;    /* :1012-1014 */
+      rw->generated++;
+      emitted++;
+      fin = finish_of(rw, tok);                                           /* Scheduler.swift:381-387 */
+      if (fin) break;
+    }
+    rw->cur = out[n_emit - 1];
+    out_counts[r] = emitted;
+    out_finish[r] = fin;
+    if (fin) rw->active = 0;                                              /* Scheduler.swift:413-427 */
+    produced++;
+  }
+  free(rows); free(counts); free(drafts); free(nprop); free(toks); free(lg);
+  return produced;
+}
+
+void or_generator_stats(or_generator* g, or_stats* out) { *out = g->stats; }
+
+int or_generator_call_widths(or_generator* g, int32_t* out, int cap) {
+  int n = g->n_widths < cap ? g->n_widths : cap;
+  memcpy(out, g->widths, sizeof(int32_t) * (size_t)n);
+  return g->n_widths;
+}
+
+int or_generator_active(or_generator* g, int row) { return g->rows[row].active; }
+
+int or_generator_history(or_generator* g, int row, int32_t* out, int cap) {
+  const or_row* rw = &g->rows[row];
+  int n = rw->hist_len < cap ? rw->hist_len : cap;
+  memcpy(out, rw->hist, sizeof(int32_t) * (size_t)n);
+  return rw->hist_len;
+}
