@@ -1,0 +1,178 @@
+"""Benchmark of the n-gram speculative-decode step on one MI355X.
+
+Workload (default): Qwen3-4B-shaped dense decoder (36 layers, hidden 2560, 32 q / 8 kv
+heads, head_dim 128, intermediate 9728, vocab 151936, tied embeddings), random-init
+weights in MLX 4-bit affine g64 format with bf16 scales/biases, batch 1, greedy,
+n-gram drafts with K=5 and match length 3, a 2048-token seeded prompt with 40% of its
+positions copied from earlier spans.  A step is one speculative step (n-gram proposal,
+(K+1)-token verify forward, acceptance, KV rollback); the prompt is prefilled before
+the timed region.  The same workload at batch 8 is reported beside it.
+
+Prints one JSON line: accepted tokens/s at batch 1 (value), the batch-8 figure, the
+verify-step latency, the live HBM roofline of the dominant kernel (the dequant GEMV,
+timed with HIP events on its stream) and the CPU oracle timed on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+QWEN3_4B = dict(arch=0, n_layers=36, hidden=2560, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=9728,
+                vocab=151936, tied_embeddings=1, rms_eps=1e-6, rope_theta=1e6, n_experts=0, n_experts_per_tok=0,
+                moe_intermediate=0)
+K_DRAFT, MATCH, PROMPT_LEN, SEED = 5, 3, 2048, 1234
+
+
+def spec_cfg(rows: int) -> dict:
+    return dict(enabled=1, max_proposal_tokens=K_DRAFT, max_suffix_tokens=MATCH, min_context_tokens=8,
+                acceptance=1, single_row_only=0, greedy_only=0)
+
+
+def step_bytes(cfg: dict, ctx_lens, M: int) -> float:
+    """Algorithmic HBM bytes of one verify step: 4-bit g64 weights at 0.5625 B/weight,
+    K/V read over each row's context, K/V written for the M verify tokens, bf16 logits."""
+    H, d, nq, nkv, I, V, L = (cfg[k] for k in ("hidden", "head_dim", "n_q_heads", "n_kv_heads", "intermediate",
+                                               "vocab", "n_layers"))
+    per_layer = (nq + 2 * nkv) * d * H + H * nq * d + 2 * I * H + H * I
+    weights = (L * per_layer + V * H) * 0.5625
+    kv_tok = L * 2 * nkv * d * 2
+    return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
+
+
+def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
+    from mlxcat_amd import _lib as hip
+    from mlxcat_amd.workloads import copy_span_prompt
+    L = hip.load()
+    if L.mc_set_device(0) < 0:
+        raise RuntimeError(L.mc_last_error().decode())
+    m = hip.Model(QWEN3_4B)
+    m.init_synthetic(SEED)
+    max_new = (warmup + steps + 8) * (K_DRAFT + 1) + 8
+    ctx = PROMPT_LEN + max_new + K_DRAFT + 16
+    b = hip.Batch(m, rows, ctx, spec_cfg(rows))
+    for r in range(rows):
+        p = copy_span_prompt(SEED + r, PROMPT_LEN, QWEN3_4B["vocab"])
+        b.insert(r, p, max_new, hip.make_sampling())
+    for _ in range(warmup):
+        b.step()
+    st0 = b.stats()
+    kv0 = [b.kv_len(r) for r in range(rows)]
+    emitted = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, c, _ = b.step()
+        emitted += int(c.sum())
+    dt = time.perf_counter() - t0
+    st1 = b.stats()
+    out = dict(tok_s=emitted / dt, ms_per_step=dt / steps * 1e3, tokens_per_step=emitted / steps / rows,
+               proposed=st1["proposed"] - st0["proposed"], accepted=st1["accepted"] - st0["accepted"],
+               batches=st1["proposal_batches"] - st0["proposal_batches"],
+               bytes_per_step=step_bytes(QWEN3_4B, kv0, rows * (K_DRAFT + 1)))
+    out["step_hbm_gbs"] = out["bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
+    if profile:
+        b.set_profiling(True)
+        g_ms = g_by = 0.0
+        g_n = 0
+        for _ in range(3):
+            b.step()
+            ms, by, n = b.profile(0)
+            g_ms += ms
+            g_by += by
+            g_n += n
+        b.set_profiling(False)
+        out["gemv"] = dict(ms=g_ms / 3, bytes=g_by / 3, launches=g_n // 3)
+    b.close()
+    m.close()
+    return out
+
+
+def run_cpu(budget_s: float = 20.0):
+    """The oracle (CPU restatement, OpenMP) on a bounded sample of the same batch-1 step:
+    synthetic K/V for the 2047 prefilled positions, then speculative steps until the
+    time budget is spent."""
+    from mlxcat_amd.workloads import copy_span_prompt
+    from oracle import pyoracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    O.lib().or_set_threads(threads)
+    p = copy_span_prompt(SEED, PROMPT_LEN, QWEN3_4B["vocab"])
+    om = O.Model(QWEN3_4B, SEED, PROMPT_LEN + 128, 1)
+    om.fill_kv(0, PROMPT_LEN - 1, 99)
+    g = O.Generator(om, spec_cfg(1), 1, PROMPT_LEN + 128)
+    g.insert_prefilled(0, p, 100, O.make_sampling())
+    g.step()  # warm-up
+    n_steps = emitted = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n_steps < 50:
+        _, c, _ = g.step()
+        emitted += int(c.sum())
+        n_steps += 1
+    dt = time.perf_counter() - t0
+    om.close()
+    return dict(value=emitted / dt, unit="tok/s", cores=threads, kind="port",
+                sample=f"{n_steps} speculative steps of the batch-1 Qwen3-4B-shape K=5 workload "
+                       f"({emitted} tokens, {dt:.1f} s) after a synthetic 2047-position KV prefill")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-b8", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
+              "(see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    b1 = run_gpu(1, a.steps, a.warmup, profile=True)
+    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False)
+    cpu = None if a.no_cpu else run_cpu()
+    g = b1["gemv"]
+    achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "accepted tok/s (bs=1,8) Qwen3-4B-shape 4-bit K=5; verify HBM GB/s %peak",
+        "value": round(b1["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(b1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init MLX 4-bit affine g64 weights, seeded copy-span prompts)",
+        "config": {"workload": "Qwen3-4B-shape 4-bit g64 n-gram speculative step, batch 1, K=5, match 3, "
+                               "2048-token prompt, greedy", "batch": 1, "k_draft": K_DRAFT, "prompt": PROMPT_LEN},
+        "tokens_per_step": round(b1["tokens_per_step"], 3),
+        "draft_hit_rate": round(b1["batches"] / a.steps, 3),
+        "accepted_drafts_per_step": round(b1["accepted"] / a.steps, 3),
+        "verify_step_ms": round(b1["ms_per_step"], 4),
+        "verify_step_hbm": {"achieved": round(b1["step_hbm_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(b1["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
+                            "bytes_per_step": b1["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qgemv_kernel<1>", "launches_per_step": g["launches"],
+                     "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 3),
+                     "alg_bytes_per_launch": round(g["bytes"] / max(1, g["launches"]))},
+        "batch8": None if b8 is None else {"tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 4),
+                                           "tokens_per_step_per_row": round(b8["tokens_per_step"], 3),
+                                           "step_hbm_frac": round(b8["step_hbm_gbs"] / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

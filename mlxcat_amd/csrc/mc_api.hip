@@ -1025,12 +1025,16 @@ extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const
                          const uint64_t* counter, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
                          int32_t* kv_keep, int32_t* n_accepted) {
   if (!logits || !row_off || !n_draft || !sp || !counter || !out_tokens || !n_emit || !kv_keep || !n_accepted || B <= 0 ||
-      vocab <= 0)
+      vocab <= 0 || row_off[0] != 0 || draft_stride < 0 || (!drafts && draft_stride > 0))
     return fail(MC_E_INVALID, "mc_accept: bad argument");
   int K = 0;
   for (int r = 0; r < B; ++r) {
     if (n_draft[r] < 0 || n_draft[r] > draft_stride) return fail(MC_E_INVALID, "mc_accept: bad n_draft");
     if (row_off[r + 1] - row_off[r] != n_draft[r] + 1) return fail(MC_E_INVALID, "mc_accept: row_off must give n_draft+1 rows");
+    for (int j = 0; j < n_draft[r]; ++j) {
+      const int32_t t = drafts[(size_t)r * draft_stride + j];
+      if (t < 0 || t >= vocab) return fail(MC_E_INVALID, "mc_accept: draft token out of range");
+    }
     K = std::max(K, n_draft[r]);
   }
   MC_HIP(hipSetDevice(g_device));

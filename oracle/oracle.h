@@ -93,6 +93,20 @@ uint64_t or_dist_mass(const or_dist* d, const uint16_t* logits, float inv_temp, 
 int or_dist_sample(const or_dist* d, const uint16_t* logits, int V, float inv_temp, uint32_t u,
                    int exclude);
 
+struct or_sampling;
+/* Acceptance of one row's verify block: lg holds P+1 logits rows (position j scores
+ * the token after verify token j), dr the P drafts.  Greedy rows (temperature 0) use
+ * `acceptance` (OR_ACCEPT_ALL_OR_NOTHING restates BatchGenerator.swift:906-947, where a
+ * rejection falls back to a one-token decode whose logits are position 0); rows with
+ * temperature > 0 use speculative sampling with the uniforms of (seed, counter).
+ * forced_cap >= 0 caps the accepted drafts (forced accept-length schedule), -1 = none.
+ * Writes the emitted tokens to out and returns their count; *kv_keep = verified
+ * positions kept in the KV, *n_acc = drafts accepted (the SpeculativeDecodingStats
+ * increment, :952), *rejected = 1 when a proposal was (partly) rejected (:938). */
+int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const struct or_sampling* sp,
+                  uint64_t seed, uint64_t counter, int acceptance, int forced_cap, int32_t* out,
+                  int* kv_keep, int* n_acc, int* rejected);
+
 /* ---- KV trim known answer: BatchCache.swift:403-424 ---- */
 /* Uniform trim of a left-padded batch: returns trimmed count, updates idx,
  * left_padding[] and offsets[] in place. */
@@ -140,6 +154,11 @@ int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t*
                      const int32_t* tokens, uint16_t* logits, uint16_t* hidden);
 
 void or_set_threads(int n);
+
+/* y[M][N] = x[M][K] . dequant(W)^T for one MLX 4-bit affine g64 tensor (fp32 in/out);
+ * the same per-output fixed-order reduction the forward uses. */
+void or_qmatmul(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                const float* x, int M, float* y);
 
 /* ---- generator + scheduler restatement ---- */
 enum { OR_ACCEPT_ALL_OR_NOTHING = 0, OR_ACCEPT_PREFIX = 1 };

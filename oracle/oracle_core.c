@@ -244,6 +244,97 @@ static int accept_draft(const or_dist* d, const uint16_t* logits, float inv_temp
 }
 
 /* ------------------------------------------------------------------ */
+/* acceptance of one row's verify block                                 */
+/* ------------------------------------------------------------------ */
+static int is_eos_tok(const or_sampling* sp, int tok) {
+  for (int i = 0; i < sp->n_eos; ++i)
+    if (sp->eos[i] == tok) return 1;
+  return 0;
+}
+
+int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_sampling* sp, uint64_t seed,
+                  uint64_t counter, int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc,
+                  int* rejected) {
+  const int sampled = sp->temperature != 0.0f;
+  const float inv_t = sampled ? 1.0f / sp->temperature : 0.0f;
+  int n_emit = 0;
+  *kv_keep = 1;
+  *n_acc = 0;
+  *rejected = 0;
+  if (!sampled && acceptance == OR_ACCEPT_ALL_OR_NOTHING) {
+    /* BatchGenerator.swift:906-947 */
+    if (P == 0) {                                                  /* plain decodeOneToken */
+      out[0] = or_argmax_bf16(lg, V);
+      return 1;
+    }
+    int all = 1, na = 0;
+    for (int pos = 0; pos <= P; ++pos) {
+      const int s = or_argmax_bf16(lg + (size_t)pos * V, V);
+      if (sp->reject_token >= 0 && s == sp->reject_token) { all = 0; break; }  /* :920-923 */
+      if (pos < P && s != dr[pos]) { all = 0; break; }                         /* :925-928 */
+      out[na++] = s;
+      if (is_eos_tok(sp, s)) break;                                            /* :932-934 */
+    }
+    if (!all) {
+      *rejected = 1;                                               /* :938 */
+      /* :939 decodeOneToken on the original cache: the same logits as position 0 */
+      out[0] = or_argmax_bf16(lg, V);
+      return 1;
+    }
+    *kv_keep = P + 1;                                              /* :942 adopt the working cache */
+    *n_acc = na > 1 ? na - 1 : 0;                                  /* :952 */
+    return na;
+  }
+  /* prefix acceptance (greedy) and speculative sampling (temperature > 0): accept drafts
+   * while they agree, emit the correction (or the bonus token after a full accept), keep
+   * the current token + accepted drafts in the KV.  forced_cap >= 0 caps the accepted
+   * drafts (forced accept-length schedule). */
+  int cap = P;
+  if (forced_cap >= 0 && forced_cap < cap) cap = forced_cap;
+  int a = 0, stop = 0;
+  for (int pos = 0; pos < P; ++pos) {
+    const uint16_t* row_lg = lg + (size_t)pos * V;
+    int tok;
+    if (!sampled) {
+      tok = or_argmax_bf16(row_lg, V);
+      if (pos >= cap || tok != dr[pos] || tok == sp->reject_token) {
+        out[n_emit++] = tok;
+        stop = 1;
+        break;
+      }
+    } else {
+      or_dist d;
+      or_dist_build(row_lg, V, sp->temperature, sp->top_p, &d);
+      const int ok = pos < cap && accept_draft(&d, row_lg, inv_t, dr[pos],
+                                               or_uniform_u32(seed, counter, (uint32_t)pos, 0));
+      if (!ok) {
+        out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t, or_uniform_u32(seed, counter, (uint32_t)pos, 1), dr[pos]);
+        stop = 1;
+        break;
+      }
+      tok = dr[pos];
+    }
+    out[n_emit++] = tok;
+    a++;
+    if (tok == sp->reject_token || is_eos_tok(sp, tok)) { stop = 1; break; }
+  }
+  if (!stop) {
+    const uint16_t* row_lg = lg + (size_t)P * V;
+    if (sampled) {
+      or_dist d;
+      or_dist_build(row_lg, V, sp->temperature, sp->top_p, &d);
+      out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t, or_uniform_u32(seed, counter, (uint32_t)P, 1), -1);
+    } else {
+      out[n_emit++] = or_argmax_bf16(row_lg, V);
+    }
+  }
+  *kv_keep = a + 1;
+  *n_acc = a;
+  *rejected = (P > 0 && a < P) ? 1 : 0;
+  return n_emit;
+}
+
+/* ------------------------------------------------------------------ */
 /* KV trim known answer: BatchCache.swift:403-424                       */
 /* ------------------------------------------------------------------ */
 int or_batch_trim(int* idx, int B, int32_t* lp, int32_t* off, int n) {
@@ -454,83 +545,14 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
   for (int i = 0, t0 = 0; i < nr; t0 += counts[i], ++i) {
     const int r = rows[i], P = nprop[r];
     or_row* rw = &g->rows[r];
-    const int32_t* dr = drafts + (size_t)r * (K + 1);
     int32_t* out = out_tokens + (size_t)r * (K + 1);
-    int n_emit = 0, kv_keep = 1;
-    const int sampled = rw->sp.temperature != 0.0f;
-    const float inv_t = sampled ? 1.0f / rw->sp.temperature : 0.0f;
-    if (!sampled && g->cfg.acceptance == OR_ACCEPT_ALL_OR_NOTHING) {
-      /* BatchGenerator.swift:906-947 */
-      int all = 1, n_acc = 0;
-      int tmp[64];
-      for (int pos = 0; pos <= P; ++pos) {
-        int s = or_argmax_bf16(lg + (size_t)(t0 + pos) * V, V);
-        if (rw->sp.reject_token >= 0 && s == rw->sp.reject_token) { all = 0; break; }  /* :920-923 */
-        if (pos < P && s != dr[pos]) { all = 0; break; }                            /* :925-928 */
-        tmp[n_acc++] = s;
-        if (is_eos(&rw->sp, s)) break;                                              /* :932-934 */
-      }
-      if (P == 0) {
-        out[0] = or_argmax_bf16(lg + (size_t)t0 * V, V);   /* decodeOneToken */
-        n_emit = 1;
-        kv_keep = 1;
-      } else if (!all) {
-        g->stats.rejected_batches++;                                  /* :938 */
-        /* :939 decodeOneToken on the original cache == position 0 of the verify */
-        out[0] = or_argmax_bf16(lg + (size_t)t0 * V, V);
-        n_emit = 1;
-        kv_keep = 1;
-      } else {
-        for (int z = 0; z < n_acc; ++z) out[z] = tmp[z];
-        n_emit = n_acc;
-        kv_keep = P + 1;                                              /* :942 adopt working cache */
-        g->stats.accepted += n_acc - 1 > 0 ? n_acc - 1 : 0;          /* :952 */
-      }
-    } else {
-      /* prefix acceptance (greedy) and speculative sampling (temperature > 0):
-       * accept drafts while they agree, emit the correction (or the bonus token
-       * after a full accept), keep current token + accepted drafts in the KV. */
-      int cap = forced_accept ? forced_accept[r] : P;
-      if (cap > P) cap = P;
-      if (cap < 0) cap = 0;
-      int a = 0, stop = 0;
-      for (int pos = 0; pos < P; ++pos) {
-        const uint16_t* row_lg = lg + (size_t)(t0 + pos) * V;
-        int tok;
-        if (!sampled) {
-          tok = or_argmax_bf16(row_lg, V);
-          if (pos >= cap || tok != dr[pos] || tok == rw->sp.reject_token) {
-            out[n_emit++] = tok;
-            stop = 1;
-            break;
-          }
-        } else {
-          or_dist d;
-          or_dist_build(row_lg, V, rw->sp.temperature, rw->sp.top_p, &d);
-          int ok = pos < cap && accept_draft(&d, row_lg, inv_t, dr[pos],
-                                             or_uniform_u32(rw->seed, rw->counter, (uint32_t)pos, 0));
-          if (!ok) {
-            out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t,
-                                           or_uniform_u32(rw->seed, rw->counter, (uint32_t)pos, 1), dr[pos]);
-            stop = 1;
-            break;
-          }
-          tok = dr[pos];
-        }
-        out[n_emit++] = tok;
-        a++;
-        if (tok == rw->sp.reject_token || is_eos(&rw->sp, tok)) { stop = 1; break; }
-      }
-      if (!stop) {
-        const uint16_t* row_lg = lg + (size_t)(t0 + P) * V;
-        out[n_emit++] = sampled ? sample_pos(rw, row_lg, V, or_uniform_u32(rw->seed, rw->counter, (uint32_t)P, 1))
-                                : or_argmax_bf16(row_lg, V);
-      }
-      kv_keep = a + 1;
-      if (P > 0) {
-        g->stats.accepted += a;
-        if (a < P) g->stats.rejected_batches++;
-      }
+    int kv_keep = 1, n_acc = 0, rejected = 0;
+    const int n_emit = or_accept_row(lg + (size_t)t0 * V, V, drafts + (size_t)r * (K + 1), P, &rw->sp, rw->seed,
+                                     rw->counter, g->cfg.acceptance, forced_accept ? forced_accept[r] : -1, out,
+                                     &kv_keep, &n_acc, &rejected);
+    if (P > 0) {
+      g->stats.accepted += n_acc;                                     /* :952 */
+      g->stats.rejected_batches += rejected;                          /* :938 */
     }
     rw->counter++;
     /* rollback: drop verified positions beyond what is kept (O(1): length only) */

@@ -263,6 +263,14 @@ static void qlinear(const or_linear* L, const float* x, int M, float* y) {
   free(xs);
 }
 
+void or_qmatmul(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                const float* x, int M, float* y) {
+  or_linear L;
+  L.N = N; L.K = K;
+  L.wq = (uint32_t*)wq; L.s = (uint16_t*)scales; L.b = (uint16_t*)biases;
+  qlinear(&L, x, M, y);
+}
+
 /* rmsnorm over n values: y = bf16((x * r) * w), r = 1/sqrt(mean(x^2) + eps) */
 static void rmsnorm(const float* x, const uint16_t* w, int n, float eps, float* out) {
   float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};

@@ -84,6 +84,8 @@ def lib():
             "or_dist_mass": (U64, [P, P, F, I]),
             "or_dist_sample": (I, [P, P, I, F, U32, I]),
             "or_batch_trim": (I, [P, I, P, P, I]),
+            "or_accept_row": (I, [P, I, P, I, P, U64, U64, I, I, P, P, P, P]),
+            "or_qmatmul": (None, [P, P, P, I, I, P, I, P]),
             "or_model_create": (P, [P, U64, I, I]),
             "or_model_destroy": (None, [P]),
             "or_model_linear": (I, [P, I, I, I, P, P, P, P, P]),
@@ -146,6 +148,33 @@ def gen_linear(seed: int, tid: int, N: int, K: int, scale_exp: int = -7):
     b = np.zeros((N, K // 64), dtype=np.uint16)
     lib().or_gen_linear(seed, tid, N, K, scale_exp, _p(wq), _p(s), _p(b))
     return wq, s, b
+
+
+def qmatmul(wq, s, b, x) -> np.ndarray:
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N, K = wq.shape[0], wq.shape[1] * 8
+    M = x.shape[0]
+    y = np.zeros((M, N), dtype=np.float32)
+    lib().or_qmatmul(_p(wq), _p(s), _p(b), N, K, _p(x), M, _p(y))
+    return y
+
+
+def accept_row(logits_bf16: np.ndarray, drafts, sampling: "Sampling", seed: int, counter: int, acceptance: int,
+               forced_cap: int = -1):
+    """Acceptance of one row: logits_bf16 [P+1][V] uint16, drafts P tokens.
+    Returns (emitted tokens, kv_keep, n_accepted, rejected)."""
+    lg = np.ascontiguousarray(logits_bf16, dtype=np.uint16)
+    dr = i32(drafts) if len(drafts) else np.zeros(1, dtype=np.int32)
+    P = len(drafts)
+    assert lg.shape[0] == P + 1
+    out = np.zeros(P + 1, dtype=np.int32)
+    keep, nacc, rej = C.c_int(), C.c_int(), C.c_int()
+    n = lib().or_accept_row(_p(lg), lg.shape[1], _p(dr), P, C.byref(sampling), seed, counter, acceptance,
+                            forced_cap, _p(out), C.byref(keep), C.byref(nacc), C.byref(rej))
+    return out[:n].tolist(), keep.value, nacc.value, rej.value
 
 
 def dist_build(logits_bf16: np.ndarray, temperature: float, top_p: float) -> Dist:

@@ -1,0 +1,57 @@
+"""Shared shapes, tolerances and helpers of the parity tests."""
+from __future__ import annotations
+
+import numpy as np
+
+# bf16 verify-logit tolerance (absolute, relative)
+ATOL, RTOL = 2e-2, 1e-2
+
+ARCH_QWEN3, ARCH_LLAMA = 0, 1
+ARCH_FAKE_REPEATING, ARCH_FAKE_MISMATCHING = 100, 101
+
+
+def cfg(arch, n_layers, hidden, nq, nkv, d, inter, vocab, tied, theta, eps=1e-6):
+    return dict(arch=arch, n_layers=n_layers, hidden=hidden, n_q_heads=nq, n_kv_heads=nkv, head_dim=d,
+                intermediate=inter, vocab=vocab, tied_embeddings=tied, rms_eps=eps, rope_theta=theta,
+                n_experts=0, n_experts_per_tok=0, moe_intermediate=0)
+
+
+# the tiny Qwen3-style decoder (2 layers, hidden 256, 4 q / 2 kv heads, head_dim 64)
+TINY = cfg(ARCH_QWEN3, 2, 256, 4, 2, 64, 704, 4096, 1, 1e6)
+# Llama-style tiny decoder (no q/k norm, untied head)
+TINY_LLAMA = cfg(ARCH_LLAMA, 2, 256, 4, 2, 64, 704, 4096, 0, 5e5)
+# the reference's scheduler test doubles (vocab 8)
+FAKE_REPEATING = cfg(ARCH_FAKE_REPEATING, 1, 64, 1, 1, 64, 64, 8, 1, 1e6)
+FAKE_MISMATCHING = cfg(ARCH_FAKE_MISMATCHING, 1, 64, 1, 1, 64, 64, 8, 1, 1e6)
+# Qwen3-4B layer shapes with 2 layers (every GEMV shape of the full model incl. the 151936-row head)
+QWEN3_4B_2L = cfg(ARCH_QWEN3, 2, 2560, 32, 8, 128, 9728, 151936, 1, 1e6)
+# Llama-3-8B layer shapes with 1 layer
+LLAMA3_8B_1L = cfg(ARCH_LLAMA, 1, 4096, 32, 8, 128, 14336, 128256, 0, 5e5)
+
+
+def spec(enabled=True, k=4, max_suffix=16, min_ctx=8, acceptance=0, single_row_only=1, greedy_only=1):
+    return dict(enabled=int(enabled), max_proposal_tokens=k, max_suffix_tokens=max_suffix, min_context_tokens=min_ctx,
+                acceptance=acceptance, single_row_only=single_row_only, greedy_only=greedy_only)
+
+
+def bf16_to_f32(a) -> np.ndarray:
+    return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a) -> np.ndarray:
+    u = np.ascontiguousarray(np.asarray(a, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def assert_close_bf16(got_u16, want_u16, atol=ATOL, rtol=RTOL, what=""):
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    w = bf16_to_f32(want_u16).astype(np.float64)
+    err = np.abs(g - w)
+    bad = err > atol + rtol * np.abs(w)
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outside {atol} abs + {rtol} rel; "
+                           f"max err {err.max():.4g}")
+
+
+def top2_margin(logits_u16_row) -> float:
+    v = np.sort(bf16_to_f32(logits_u16_row).astype(np.float64))
+    return float(v[-1] - v[-2])
