@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -123,7 +124,7 @@ extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: architecture not supported by this build");
   }
-  if (c.n_layers <= 0 || c.hidden % 64 || c.head_dim > 128 || c.head_dim % 2 || c.n_kv_heads <= 0 ||
+  if (c.n_layers <= 0 || c.hidden % 64 || c.hidden > 4096 || c.head_dim > 128 || c.head_dim % 16 || c.n_kv_heads <= 0 ||
       c.n_q_heads % c.n_kv_heads || c.intermediate % 64 || c.vocab <= 0 || (c.n_q_heads * c.head_dim) % 64) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: unsupported shape");
@@ -339,10 +340,11 @@ struct mc_batch {
   std::vector<KVLayer> kv;
   uint16_t* kv_mem = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
-  uint16_t *x = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *act = nullptr,
+  uint16_t *x = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *act = nullptr,
            *logits = nullptr;
   float* gemv_part = nullptr;
   unsigned* gemv_cnt = nullptr;
+  float* ssq = nullptr;  // [hidden / 16][Mmax]: per-tile sums of squares of the residual stream
   AttnWork aw{};
   StepState s;
   void* scratch = nullptr;  // one allocation for the small StepState arrays
@@ -370,9 +372,9 @@ static void batch_free(mc_batch* b) {
   (void)hipSetDevice(b->m->device);
   if (b->graph) (void)hipGraphExecDestroy(b->graph);
   if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
-  for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->xn, (void*)b->qkv,
+  for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
-                  (void*)b->gemv_cnt, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
+                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -442,7 +444,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     MC_HIP(hipMemcpy(b->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
     MC_HIP(hipMemcpy(b->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     const size_t Nqkv = (size_t)(nq + 2 * nkv) * d;
-    if ((rc = dev_zero(&b->x, (size_t)M * H)) || (rc = dev_zero(&b->xn, (size_t)M * std::max(H, I))) ||
+    if ((rc = dev_zero(&b->x, (size_t)M * H)) ||
         (rc = dev_zero(&b->qkv, (size_t)M * Nqkv)) || (rc = dev_zero(&b->q, (size_t)M * nq * d)) ||
         (rc = dev_zero(&b->att, (size_t)M * nq * d)) || (rc = dev_zero(&b->act, (size_t)M * I))) {
       batch_free(b);
@@ -453,15 +455,19 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     int maxnt = 1;
     auto acc_plan = [&](const QLinear& L) {
       for (int MT = 1; MT <= 4; ++MT) {
-        int gpr, ks;
-        gemv_plan(L, MT, &gpr, &ks);
+        int kr, ks;
+        gemv_plan(L, MT, &kr, &ks);
         if (ks > 1) part = std::max(part, (size_t)ks * L.NT * MT * 64 * 4);
       }
       maxnt = std::max(maxnt, L.NT);
     };
     for (auto& L : m->layers) { acc_plan(L.qkv); acc_plan(L.o); acc_plan(L.gateup); acc_plan(L.down); }
     acc_plan(m->head());
-    if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt))) { batch_free(b); return rc; }
+    if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt)) ||
+        (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M))) {
+      batch_free(b);
+      return rc;
+    }
     b->aw.nchunk = (max_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     if ((rc = dev_alloc(&b->aw.part_o, (size_t)M * nq * b->aw.nchunk * d)) ||
         (rc = dev_alloc(&b->aw.part_ml, (size_t)M * nq * b->aw.nchunk * 2))) {
@@ -534,16 +540,26 @@ static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
   return MC_OK;
 }
 
-static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, uint16_t* y, int ldy, int M, int epi) {
+// One linear over M tokens, in launches of at most 64.  norm_w != NULL fuses the
+// RMSNorm of the input rows (their sums of squares are the per-tile partials in b->ssq);
+// EPI_RESIDUAL writes the new rows' partials to b->ssq for the next norm.
+static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, const uint16_t* norm_w, float eps,
+                    uint16_t* y, int ldy, int M, int epi, int ss_m0 = 0) {
+  const int H = b->m->cfg.hidden;
   for (int m0 = 0; m0 < M; m0 += 64) {
     const int mc = std::min(64, M - m0);
     const int MT = (mc + 15) / 16;
     GemvArgs a;
     a.qw = L.qw; a.sb = L.sb;
     a.x = x + (size_t)m0 * ldx; a.ldx = ldx;
+    if (norm_w) {
+      a.norm_w = norm_w; a.eps = eps;
+      a.ss_in = b->ssq + ss_m0 + m0; a.ss_nt = H / 16; a.ss_ld = b->Mmax;
+    }
+    if (epi == EPI_RESIDUAL) { a.ss_out = b->ssq + ss_m0 + m0; a.ss_ld_out = b->Mmax; }
     a.y = y + (size_t)m0 * ldy; a.ldy = ldy;
     a.M = mc; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
-    gemv_plan(L, MT, &a.gpr, &a.ksplit);
+    gemv_plan(L, MT, &a.kr, &a.ksplit);
     a.part = b->gemv_part; a.counters = b->gemv_cnt; a.epi = epi;
     size_t e0 = 0;
     int rc = prof_begin(b, &e0);
@@ -568,11 +584,10 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
-  if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->st))) return rc;
+  if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->ssq, b->Mmax, b->st))) return rc;
   for (int l = 0; l < c.n_layers; ++l) {
     const auto& L = m->layers[(size_t)l];
-    if ((rc = launch_rmsnorm(b->x, L.in_norm, M, H, c.rms_eps, b->xn, b->st))) return rc;
-    if ((rc = run_gemv(b, L.qkv, b->xn, H, b->qkv, Nqkv, M, EPI_STORE))) return rc;
+    if ((rc = run_gemv(b, L.qkv, b->x, H, L.in_norm, c.rms_eps, b->qkv, Nqkv, M, EPI_STORE))) return rc;
     if ((rc = launch_qk_rope_append(b->qkv, L.q_norm, L.k_norm, b->rope_cos, b->rope_sin, M, nq, nkv, d, c.rms_eps,
                                     s.slot_row, s.slot_pos, b->kv[(size_t)l], b->q, b->st)))
       return rc;
@@ -581,14 +596,14 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
     if ((rc = launch_attention(b->q, b->kv[(size_t)l], sv, b->R, max_q, nq, nkv, d, M, b->aw, b->att, b->st)))
       return rc;
     if ((rc = prof_end(b, e0, 1, 0.0))) return rc;
-    if ((rc = run_gemv(b, L.o, b->att, nq * d, b->x, H, M, EPI_RESIDUAL))) return rc;
-    if ((rc = launch_rmsnorm(b->x, L.post_norm, M, H, c.rms_eps, b->xn, b->st))) return rc;
-    if ((rc = run_gemv(b, L.gateup, b->xn, H, b->act, I, M, EPI_SWIGLU))) return rc;
-    if ((rc = run_gemv(b, L.down, b->act, I, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if ((rc = run_gemv(b, L.o, b->att, nq * d, nullptr, 0.f, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if ((rc = run_gemv(b, L.gateup, b->x, H, L.post_norm, c.rms_eps, b->act, I, M, EPI_SWIGLU))) return rc;
+    if ((rc = run_gemv(b, L.down, b->act, I, nullptr, 0.f, b->x, H, M, EPI_RESIDUAL))) return rc;
   }
   if (lgn > 0) {
-    if ((rc = launch_rmsnorm(b->x + (size_t)lg0 * H, m->final_norm, lgn, H, c.rms_eps, b->xn, b->st))) return rc;
-    if ((rc = run_gemv(b, m->head(), b->xn, H, b->logits + (size_t)lg0 * c.vocab, c.vocab, lgn, EPI_STORE))) return rc;
+    if ((rc = run_gemv(b, m->head(), b->x + (size_t)lg0 * H, H, m->final_norm, c.rms_eps, b->logits + (size_t)lg0 * c.vocab,
+                       c.vocab, lgn, EPI_STORE, lg0)))
+      return rc;
   }
   return MC_OK;
 }
@@ -897,7 +912,15 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
       for (int r = 0; r < R; ++r) f[(size_t)r] = forced_accept[r] < 0 ? -1 : forced_accept[r];
     if ((rc = upload_i32(b, b->s.forced, f.data(), (size_t)R))) return rc;
   }
-  if (b->profiling) {
+  // MC_STEP_EAGER=1 launches the step's kernels directly instead of replaying the captured
+  // graph (same kernels; used under profilers that do not follow graph launches).
+  static const bool eager = [] {
+    const char* e = getenv("MC_STEP_EAGER");
+    return e && e[0] == '1';
+  }();
+  if (eager && !b->profiling) {
+    if ((rc = enqueue_step(b))) return rc;
+  } else if (b->profiling) {
     b->ev_used = 0;
     b->recs.clear();
     size_t e0 = 0;

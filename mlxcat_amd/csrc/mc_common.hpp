@@ -108,8 +108,8 @@ __device__ inline uint64_t mass_of(float e) {
 // (w >> 4p) & 0x000F000F | 0x43004300 yields the bf16 pair (128 + q_2p, 128 + q_2p+1).
 //
 // Scales/biases: uint32 (scale bf16 | bias bf16 << 16) at
-// sb[((t * GP + gp) * 4 + c) * 8 + gi * 4 + v] for row 16t + 4c + v, group 2gp + gi,
-// which is the 4 output rows a lane holds in the MFMA accumulator layout.
+// sb[((t * GP + gp) * 16 + r) * 2 + gi] for row 16t + r, group 2gp + gi: the lane that
+// owns weight row r of the tile reads its two groups with one 8-byte load.
 // Rows >= N and groups >= K/64 are zero (scale = bias = 0, so they add nothing).
 // ---------------------------------------------------------------------------
 struct QLinear {

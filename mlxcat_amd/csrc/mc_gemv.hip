@@ -3,18 +3,27 @@
 //
 // Y[M, N] = X[M, K] . W^T with W = s*q + b per group of 64 inputs (MLX affine
 // quantisation, the `quantizedMatmul` every QuantizedLinear runs in the verify
-// forward).  Bandwidth-bound at small M, so the design streams the packed weights
-// once with 16-byte lane loads (1 KiB per wave per group pair), keeps X in LDS,
-// and multiplies on the matrix cores:
-//   * the nibbles become exact bf16 values 128 + q with one shift and one and-or
-//     per pair (no int->float conversion),
-//   * v_mfma_f32_16x16x32_bf16 computes sum_k x_k (128 + q_k) per group exactly
-//     (bf16 products are exact in fp32),
-//   * y += s * acc_g + (b - 128 s) * xsum_g folds the affine scale/bias per group,
-//     with xsum_g = sum_k x_k precomputed once per block in LDS.
-// Each output's reduction order depends only on (N, K) -- never on M -- so a
-// token's result is bit-identical whether it is verified alone or with drafts.
+// forward).  At verify sizes (M = rows x (K+1) <= 64) the op is bound by streaming
+// the packed weights from HBM, so the kernel is built around memory-level
+// parallelism:
+//   * one block = one 16-row tile x one K-range; each wave issues every 16-byte
+//     weight load it will need (up to 5 group pairs = 5 KiB per wave) before it
+//     touches anything else, so a CU keeps tens of KiB in flight;
+//   * the activations of the K-range are staged in LDS while the weights are in
+//     flight; an optional RMSNorm over the full input row is fused into that staging;
+//   * nibbles become exact bf16 values 128 + q with one shift and one and-or per
+//     pair, and v_mfma_f32_16x16x32_bf16 forms sum_k x_k (128 + q_k) per group;
+//     y += s * acc + (b - 128 s) * sum_k x_k folds in the affine scale/bias;
+//   * split-K partials travel through device-coherent (sc1) stores and loads with
+//     an arrival counter per tile, so no L2 writeback/invalidate fence is needed;
+//     the last-arriving block reduces them in K-range order and runs the epilogue
+//     (store, residual add, or SwiGLU of interleaved gate/up rows).
+// The K-range plan depends only on (N, K) and the M class (M <= 16 or M <= 64), and
+// every reduction runs in a fixed order, so a token's result is bit-identical
+// whatever the number of tokens in the launch (within the class).
 #include "mc_gemv.hpp"
+
+#include <algorithm>
 
 namespace mc {
 
@@ -22,261 +31,483 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ inline bf16x8 dequant_word(uint32_t w) {
+// mask = 0x000F000F, magic = 0x43004300, passed in registers so that each pair becomes
+// one v_and_or_b32 (VOP3 takes no literal operands on this architecture)
+__device__ inline bf16x8 dequant_word(uint32_t w, uint32_t mask, uint32_t magic) {
   u32x4 p;
-  p.x = (w & 0x000F000Fu) | 0x43004300u;
-  p.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  p.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  p.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  p.x = (w & mask) | magic;
+  p.y = ((w >> 4) & mask) | magic;
+  p.z = ((w >> 8) & mask) | magic;
+  p.w = ((w >> 12) & mask) | magic;
   return __builtin_bit_cast(bf16x8, p);
 }
 
 __device__ inline float silu_f(float z) { return z / (1.0f + __expf(-z)); }
 
-// LDS row stride (bf16 elements) of the X tile: +8 elements (16 B) of padding so
-// the 16 lanes that read one k-slot block from 16 different rows spread over banks.
-__host__ __device__ constexpr int xrow_stride(int gpr) { return gpr * 128 + 8; }
+// device-coherent 64-bit store / load (relaxed, agent scope: sc1 accesses)
+__device__ inline void st_coherent(float* p, float a, float b) {
+  const unsigned long long v = (unsigned long long)__float_as_uint(a) | ((unsigned long long)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 ld_coherent(const float* p) {
+  const unsigned long long v =
+      __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for
+// its outstanding global loads (__syncthreads would also drain the prefetched weights).
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// LDS row stride (bf16 elements) of the X tile: +8 elements (16 B) of padding so the
+// 16 lanes that read one k-slot block from 16 different rows spread over banks.
+__host__ __device__ constexpr int xrow_stride(int kr) { return kr * 128 + 8; }
 
 constexpr int GEMV_WAVES = 4;
-constexpr int GEMV_LDS_LIMIT = 64 * 1024;
+constexpr int GEMV_LDS_LIMIT = 160 * 1024;
 
-// One block = one 16-row tile x one K-range of `gpr` group pairs; its 4 waves take
-// the range's group pairs round-robin (so the block streams one contiguous run of
-// 1 KiB blocks), then reduce through LDS in wave order.  With ksplit > 1 the K-range
-// partials go to a workspace and the last block of a tile sums them in kr order.
-// X rows m < M are staged in LDS; lanes of columns m >= M read a zero row.
-template <int MT>
-__global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int gpr = a.gpr;
-  const int XS = xrow_stride(gpr);
-  const int Mr = a.M < 16 * MT ? a.M : 16 * MT;                           // staged rows
-  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                        // [Mr + 1][XS]
-  float* xsum = reinterpret_cast<float*>(smem + (size_t)(16 * MT + 1) * XS * 2);  // [16*MT + 1][2*gpr]
-  float* red = xsum + (16 * MT + 1) * 2 * gpr;                             // [4 waves][MT][64][4]
+size_t gemv_lds_bytes(int Mr, int kr, int MT) {
+  return (size_t)Mr * xrow_stride(kr) * 2 + (size_t)16 * MT * 2 * kr * 4 + (size_t)2 * GEMV_WAVES * MT * 64 * 16 +
+         64 * 4 + (size_t)kr * 128 * 2;
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int t = blockIdx.x, kr = blockIdx.y;
-  const int gp0 = kr * gpr;
-  const int gp1 = min(a.GP, gp0 + gpr);
-  const int ngp = gp1 - gp0;
-  const int k0 = gp0 * 128;
-  const int ng = ngp * 2;
+// Weight registers of one work unit (tile x K-range) for one wave: D group pairs.
+template <int D>
+struct WBuf {
+  u32x4 nib[D];
+  uint2 sb[D];  // (scale | bias << 16) of this lane's weight row, groups 2gp and 2gp + 1
+};
 
-  // ---- stage X[0:Mr][k0 : k0 + ngp*128] and a zero row into LDS ----
-  {
-    const int cpr = ngp * 16;  // 16-byte chunks per row
-    const int total = (Mr + 1) * cpr;
-    for (int i = tid; i < total; i += 256) {
-      const int m = i / cpr, ch = i - m * cpr;
-      const int k = k0 + ch * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < Mr && k < a.K) v = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k);
-      *reinterpret_cast<u32x4*>(xl + m * XS + ch * 8) = v;
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < (Mr + 1) * ng; i += 256) {
-    const int m = i / ng, gl = i - m * ng;
-    const uint16_t* p = xl + m * XS + gl * 64;
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+template <int D>
+__device__ inline void load_unit(WBuf<D>& w, const GemvArgs& a, int t, int gp0, int ngp, int wave, int lane, int r16) {
+  const u32x4* qbase = reinterpret_cast<const u32x4*>(a.qw) + ((size_t)t * a.GP + gp0) * 64 + lane;
+  const uint2* sbase = reinterpret_cast<const uint2*>(a.sb) + ((size_t)t * a.GP + gp0) * 16 + r16;
 #pragma unroll
-    for (int k = 0; k < 64; k += 4) {
-      s0 += bf16_to_f32(p[k]);
-      s1 += bf16_to_f32(p[k + 1]);
-      s2 += bf16_to_f32(p[k + 2]);
-      s3 += bf16_to_f32(p[k + 3]);
-    }
-    xsum[m * ng + gl] = (s0 + s1) + (s2 + s3);
+  for (int i = 0; i < D; ++i) {
+    const int j = min(wave + GEMV_WAVES * i, ngp - 1);  // a short K-range re-reads its last pair
+    w.nib[i] = __builtin_nontemporal_load(qbase + (size_t)j * 64);
+    w.sb[i] = sbase[(size_t)j * 16];
   }
-  __syncthreads();
+}
 
-  const int c = lane >> 4, r16 = lane & 15;
-  f32x4 acc[MT];
+// Sum over this wave's group pairs of one unit.  The activations are the MFMA's A
+// operand (rows = tokens) and the weights its B operand (columns = weight rows), so lane
+// (c, r16) ends with tokens mt*16 + 4c + v (v = 0..3) of weight row 16t + r16 and applies
+// one row's scale and bias.  xsum is laid out [group][16 * MT tokens].
+template <int MT, int D>
+__device__ inline void compute_unit(f32x4 (&acc)[MT], const WBuf<D>& w, const uint16_t* xl, const float* xsum, int XS,
+                                    int Mr, int ngp, int wave, int c, int r16, uint32_t mask, uint32_t magic) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  // column of this lane per m-tile: its staged row, or the zero row
-  int xr[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xr[mt] = (mt * 16 + r16 < Mr) ? (mt * 16 + r16) : Mr;
-
-  const u32x4* qbase = reinterpret_cast<const u32x4*>(a.qw) + ((size_t)t * a.GP + gp0) * 64 + lane;
-  const u32x4* sbase = reinterpret_cast<const u32x4*>(a.sb) + (((size_t)t * a.GP + gp0) * 4 + c) * 2;
-
-  auto compute = [&](int j, const u32x4& nib, const u32x4& sc0, const u32x4& sc1) {
+  for (int i = 0; i < D; ++i) {
+    const int j = wave + GEMV_WAVES * i;
+    if (j >= ngp) break;
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
-      const bf16x8 wv0 = dequant_word(gi ? nib.z : nib.x);
-      const bf16x8 wv1 = dequant_word(gi ? nib.w : nib.y);
-      const u32x4 scv = gi ? sc1 : sc0;
+      const bf16x8 wv0 = dequant_word(gi ? w.nib[i].z : w.nib[i].x, mask, magic);
+      const bf16x8 wv1 = dequant_word(gi ? w.nib[i].w : w.nib[i].y, mask, magic);
+      const uint32_t sbv = gi ? w.sb[i].y : w.sb[i].x;
+      const float sv = __uint_as_float(sbv << 16);
+      const float bv = __builtin_fmaf(-128.0f, sv, __uint_as_float(sbv & 0xFFFF0000u));
       const int kl = j * 128 + gi * 64;
       const int gl = j * 2 + gi;
-      float sv[4], bv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        sv[v] = bf16_to_f32((uint16_t)(scv[v] & 0xFFFFu));
-        bv[v] = bf16_to_f32((uint16_t)(scv[v] >> 16)) - 128.0f * sv[v];
-      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint16_t* xrow = xl + xr[mt] * XS + kl + 8 * c;
+        // token rows >= M read row Mr - 1: finite values whose results are never stored
+        const int m = min(mt * 16 + r16, Mr - 1);
+        const uint16_t* xrow = xl + m * XS + kl + 8 * c;
         const bf16x8 xv0 = *reinterpret_cast<const bf16x8*>(xrow);
         const bf16x8 xv1 = *reinterpret_cast<const bf16x8*>(xrow + 32);
         f32x4 g = {0.f, 0.f, 0.f, 0.f};
-        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv0, xv0, g, 0, 0, 0);
-        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv1, xv1, g, 0, 0, 0);
-        const float xs = xsum[xr[mt] * ng + gl];
+        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv0, wv0, g, 0, 0, 0);
+        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv1, wv1, g, 0, 0, 0);
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(xsum + gl * 16 * MT + mt * 16 + 4 * c);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[mt][v] += sv[v] * g[v] + bv[v] * xs;
+        for (int v = 0; v < 4; ++v) {
+          acc[mt][v] = __builtin_fmaf(sv, g[v], acc[mt][v]);
+          acc[mt][v] = __builtin_fmaf(bv, xs[v], acc[mt][v]);
+        }
+      }
+    }
+  }
+}
+
+// Sum of the 4 waves' unit results, in wave order.
+template <int MT>
+__device__ inline void reduce_waves(f32x4 (&acc)[MT], const float* red, int lane) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 sacc = *reinterpret_cast<const f32x4*>(red + ((0 * MT + mt) * 64 + lane) * 4);
+#pragma unroll
+    for (int w = 1; w < GEMV_WAVES; ++w) sacc += *reinterpret_cast<const f32x4*>(red + ((w * MT + mt) * 64 + lane) * 4);
+    acc[mt] = sacc;
+  }
+}
+
+// The epilogue of one tile: lane holds tokens m = mt*16 + 4c + v of weight row n = 16t + r16.
+template <int MT>
+__device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int c, int r16) {
+  const int n = t * 16 + r16;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = mt * 16 + 4 * c + v;
+      const bool live = m < a.M;
+      if (a.epi == EPI_SWIGLU) {
+        // rows interleave (gate_i, up_i): the even lane takes up_i from its odd neighbour
+        const float up = __shfl_xor(acc[mt][v], 1);
+        if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)m * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[mt][v]) * up);
+      } else if (a.epi == EPI_RESIDUAL) {
+        // residual add, and this tile's sum of squares of the new rows for the next RMSNorm
+        // (N % 16 == 0 here: the hidden size)
+        float q = 0.f;
+        if (live) {
+          uint16_t* yp = a.y + (size_t)m * a.ldy + n;
+          const uint16_t h = f32_to_bf16(acc[mt][v] + bf16_to_f32(*yp));
+          *yp = h;
+          const float rr = bf16_to_f32(h);
+          q = rr * rr;
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
+        if (live && r16 == 0 && a.ss_out) a.ss_out[(size_t)t * a.ss_ld_out + m] = q;
+      } else if (live && n < a.N) {
+        a.y[(size_t)m * a.ldy + n] = f32_to_bf16(acc[mt][v]);
+      }
+    }
+  }
+}
+
+// Device-coherent partial of unit (t, kr); no wait here (the arrival is counted later).
+template <int MT>
+__device__ inline void store_partial(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int kr, int lane) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    float* dst = a.part + ((((size_t)kr * a.NT + t) * MT + mt) * 64 + lane) * 4;
+    st_coherent(dst, acc[mt][0], acc[mt][1]);
+    st_coherent(dst + 2, acc[mt][2], acc[mt][3]);
+  }
+}
+
+// Count this wave's arrival for tile t (its partial stores are complete); the last of the
+// ksplit arrivals sums the partials in K-range order and runs the epilogue.
+template <int MT>
+__device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16) {
+  unsigned arrived = 0u;
+  if (lane == 0) arrived = atomicAdd(a.counters + t, 1u);
+  arrived = __shfl(arrived, 0);
+  if (arrived != (unsigned)(a.ksplit - 1)) return;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int k2 = 0; k2 < a.ksplit; ++k2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float* src = a.part + ((((size_t)k2 * a.NT + t) * MT + mt) * 64 + lane) * 4;
+      const float2 p0 = ld_coherent(src), p1 = ld_coherent(src + 2);
+      acc[mt][0] += p0.x;
+      acc[mt][1] += p0.y;
+      acc[mt][2] += p1.x;
+      acc[mt][3] += p1.y;
+    }
+  }
+  if (lane == 0) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  epilogue<MT>(a, acc, t, c, r16);
+}
+
+// U work units per block: unit u = tile (u / ksplit) x K-range (u % ksplit); block b takes
+// u = b, b + G, ..., b + (U-1) G with G % ksplit == 0, so its K-range -- and the
+// activations it stages in LDS -- never change.  The next unit's weights are in flight
+// while the current one is computed; the steps are unrolled (straight-line code) and
+// every prefetch is unconditional (a block past the end re-reads the last unit), so the
+// compiler's load counters keep the prefetch outstanding during the compute.
+template <int MT, int D, int U>
+__global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int kr_gp = a.kr;
+  const int XS = xrow_stride(kr_gp);
+  const int Mr = min(a.M, 16 * MT);
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                                   // [Mr][XS]
+  float* xsum = reinterpret_cast<float*>(smem + (size_t)Mr * XS * 2);                 // [2 kr][16 MT]
+  float* red = xsum + 16 * MT * 2 * kr_gp;                                            // [2][4][MT][64][4]
+  float* rs = red + 2 * GEMV_WAVES * MT * 64 * 4;                                      // [64] row scales
+  uint16_t* wl = reinterpret_cast<uint16_t*>(rs + 64);                                 // [kr * 128] norm weights
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int G = gridDim.x, ks = a.ksplit, nunits = a.NT * ks;
+  const int kr = blockIdx.x % ks;
+  const int gp0 = kr * kr_gp;
+  const int ngp = min(a.GP, gp0 + kr_gp) - gp0;
+  const int k0 = gp0 * 128;
+  const int ng = ngp * 2;
+  const int c = lane >> 4, r16 = lane & 15;
+
+  // ---- 1. small loads first (vmcnt retires in order): norm partials and weights, X ----
+  // row scale of the fused RMSNorm: wave w reduces rows w, w + 4, ... over the producer's
+  // per-tile sums of squares, lane l taking tiles l, l + 64, ... (fixed order)
+  constexpr int RW = MT * 4;         // rows per wave, at most
+  constexpr int SL = 4;              // producer tiles per lane, at most (ss_nt <= 256)
+  float ssv[RW][SL];
+  if (a.norm_w) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int u = 0; u < SL; ++u) {
+        const int m = wave + GEMV_WAVES * r, tt = lane + 64 * u;
+        ssv[r][u] = (m < Mr && tt < a.ss_nt) ? a.ss_in[(size_t)tt * a.ss_ld + m] : 0.f;
+      }
+  }
+  constexpr int XCH = 8;             // 16-byte X chunks per thread per pass
+  const int cpr = ngp * 16;          // chunks per row in this K-range
+  u32x4 nw[2];                       // norm weights of the K-range (cpr <= 320 chunks)
+  if (a.norm_w) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = k0 + (tid + 256 * u) * 8;
+      nw[u] = (u32x4){0u, 0u, 0u, 0u};
+      if (tid + 256 * u < cpr && k < a.K) nw[u] = *reinterpret_cast<const u32x4*>(a.norm_w + k);
+    }
+  }
+  const int xtotal = Mr * cpr;
+  u32x4 xv[XCH];
+#pragma unroll
+  for (int u = 0; u < XCH; ++u) {
+    const int i = tid + 256 * u;
+    xv[u] = (u32x4){0u, 0u, 0u, 0u};
+    if (i < xtotal) {
+      const int m = i / cpr, ch = i - m * cpr;
+      if (k0 + ch * 8 < a.K) xv[u] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
+    }
+  }
+
+  // ---- 2. the first unit's weights ----
+  int u = blockIdx.x;
+  WBuf<D> wa, wb;
+  load_unit<D>(wa, a, min(u, nunits - 1) / ks, gp0, ngp, wave, lane, r16);
+
+  // ---- 3. row scales, then X (normalised) into LDS while the weights are in flight ----
+  if (a.norm_w) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (tid + 256 * q < cpr) *reinterpret_cast<u32x4*>(wl + (tid + 256 * q) * 8) = nw[q];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float q = 0.f;
+#pragma unroll
+      for (int v = 0; v < SL; ++v) q += ssv[r][v];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+      const int m = wave + GEMV_WAVES * r;
+      if (lane == 0 && m < Mr) rs[m] = 1.0f / sqrtf(q / (float)a.K + a.eps);
+    }
+    lds_barrier();
+  }
+  auto stage = [&](int base) {
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int i = base + tid + 256 * q;
+      if (i < xtotal) {
+        const int m = i / cpr, ch = i - m * cpr;
+        u32x4 v = xv[q];
+        if (a.norm_w) {
+          const float r = rs[m];
+          const u32x4 w = *reinterpret_cast<const u32x4*>(wl + ch * 8);
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const float lo = (bf16_to_f32((uint16_t)(v[h] & 0xFFFFu)) * r) * bf16_to_f32((uint16_t)(w[h] & 0xFFFFu));
+            const float hi = (bf16_to_f32((uint16_t)(v[h] >> 16)) * r) * bf16_to_f32((uint16_t)(w[h] >> 16));
+            v[h] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+          }
+        }
+        *reinterpret_cast<u32x4*>(xl + m * XS + ch * 8) = v;
       }
     }
   };
-
-  // wave takes local group pairs j = wave, wave + 4, ...; two in flight
-  {
-    int j = wave;
-    u32x4 nA = {0u, 0u, 0u, 0u}, sA0 = nA, sA1 = nA, nB = nA, sB0 = nA, sB1 = nA;
-    if (j < ngp) {
-      nA = __builtin_nontemporal_load(qbase + (size_t)j * 64);
-      sA0 = sbase[(size_t)j * 8];
-      sA1 = sbase[(size_t)j * 8 + 1];
-    }
-    while (j < ngp) {
-      const int jn = j + GEMV_WAVES;
-      if (jn < ngp) {
-        nB = __builtin_nontemporal_load(qbase + (size_t)jn * 64);
-        sB0 = sbase[(size_t)jn * 8];
-        sB1 = sbase[(size_t)jn * 8 + 1];
+  stage(0);
+  if (xtotal > 256 * XCH) {  // rare (large M x K-range): further passes, which also wait for the weights
+    for (int base = 256 * XCH; base < xtotal; base += 256 * XCH) {
+#pragma unroll
+      for (int q = 0; q < XCH; ++q) {
+        const int i = base + tid + 256 * q;
+        xv[q] = (u32x4){0u, 0u, 0u, 0u};
+        if (i < xtotal) {
+          const int m = i / cpr, ch = i - m * cpr;
+          if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
+        }
       }
-      compute(j, nA, sA0, sA1);
-      j = jn;
-      if (j >= ngp) break;
-      const int jn2 = j + GEMV_WAVES;
-      if (jn2 < ngp) {
-        nA = __builtin_nontemporal_load(qbase + (size_t)jn2 * 64);
-        sA0 = sbase[(size_t)jn2 * 8];
-        sA1 = sbase[(size_t)jn2 * 8 + 1];
-      }
-      compute(j, nB, sB0, sB1);
-      j = jn2;
+      stage(base);
     }
+    __builtin_amdgcn_s_waitcnt(0);  // leave no load of this branch pending at the merge
   }
-
-  // ---- in-block reduction over the 4 waves, in wave order ----
+  lds_barrier();
+  for (int i = tid; i < 16 * MT * ng; i += 256) {
+    const int m = i % (16 * MT), gl = i / (16 * MT);
+    const uint16_t* p = xl + min(m, Mr - 1) * XS + gl * 64;
+    float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    *reinterpret_cast<f32x4*>(red + ((wave * MT + mt) * 64 + lane) * 4) = acc[mt];
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    f32x4 s = *reinterpret_cast<const f32x4*>(red + ((0 * MT + mt) * 64 + lane) * 4);
-#pragma unroll
-    for (int w = 1; w < GEMV_WAVES; ++w) s += *reinterpret_cast<const f32x4*>(red + ((w * MT + mt) * 64 + lane) * 4);
-    acc[mt] = s;
-  }
-
-  // ---- cross-block split-K reduction (fixed order kr = 0..ksplit-1) ----
-  if (a.ksplit > 1) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float* dst = a.part + ((((size_t)kr * a.NT + t) * MT + mt) * 64 + lane) * 4;
-      *reinterpret_cast<f32x4*>(dst) = acc[mt];
+    for (int k = 0; k < 64; k += 4) {
+      q0 += bf16_to_f32(p[k]);
+      q1 += bf16_to_f32(p[k + 1]);
+      q2 += bf16_to_f32(p[k + 2]);
+      q3 += bf16_to_f32(p[k + 3]);
     }
-    __threadfence();
-    unsigned arrived = 0u;
-    if (lane == 0) arrived = atomicAdd(a.counters + t, 1u);
-    arrived = __shfl(arrived, 0);
-    if (arrived != (unsigned)(a.ksplit - 1)) return;
-    __threadfence();
+    xsum[gl * 16 * MT + m] = (q0 + q1) + (q2 + q3);
+  }
+  lds_barrier();
+
+  // ---- 4. units: prefetch the next, compute this one, reduce (waves take turns) ----
+  // A unit whose epilogue needs no load (ksplit == 1, store / SwiGLU) finishes in the loop;
+  // the others leave a coherent partial and are counted after the loop, when no prefetch
+  // is outstanding any more (vmcnt retires in order, so a wait inside the loop would
+  // also wait for the next unit's weights).
+  // one dequant constant in an SGPR, the other in a VGPR: v_and_or_b32 may read one SGPR
+  const uint32_t mask = a.dq_mask;
+  uint32_t magic;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.dq_magic));
+  const bool deferred = ks > 1 || a.epi == EPI_RESIDUAL;
+  f32x4 acc[MT];
+  const int u0 = u;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int k2 = 0; k2 < a.ksplit; ++k2) {
+  for (int step = 0; step < U; ++step) {
+    WBuf<D>& cur = (step & 1) ? wb : wa;
+    WBuf<D>& nxt = (step & 1) ? wa : wb;
+    if (step + 1 < U) load_unit<D>(nxt, a, min(u + G, nunits - 1) / ks, gp0, ngp, wave, lane, r16);
+    if (u < nunits) {  // uniform: the whole block
+      compute_unit<MT, D>(acc, cur, xl, xsum, XS, Mr, ngp, wave, c, r16, mask, magic);
+      float* rb = red + (size_t)(step & 1) * GEMV_WAVES * MT * 64 * 4;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float* src = a.part + ((((size_t)k2 * a.NT + t) * MT + mt) * 64 + lane) * 4;
-        acc[mt] += *reinterpret_cast<const f32x4*>(src);
+      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4*>(rb + ((wave * MT + mt) * 64 + lane) * 4) = acc[mt];
+      lds_barrier();
+      if (wave == (step & 3)) {
+        reduce_waves<MT>(acc, rb, lane);
+        if (deferred) store_partial<MT>(a, acc, u / ks, kr, lane);
+        else epilogue<MT>(a, acc, u / ks, c, r16);
       }
     }
-    if (lane == 0) a.counters[t] = 0u;
+    u += G;
   }
-
-  // ---- epilogue: lane holds rows n = 16t + 4c + v (v = 0..3) of column m ----
-  const int n0 = t * 16 + c * 4;
+  if (deferred) {
+    // this wave's partial stores are complete (device-visible) before its arrivals count
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + r16;
-    if (m >= a.M) continue;
-    if (a.epi == EPI_SWIGLU) {
-      // rows interleave (gate_i, up_i): outputs n0/2 and n0/2 + 1
-      const int i0 = n0 >> 1;
-      if (n0 + 1 < a.N) a.y[(size_t)m * a.ldy + i0] = f32_to_bf16(silu_f(acc[mt][0]) * acc[mt][1]);
-      if (n0 + 3 < a.N) a.y[(size_t)m * a.ldy + i0 + 1] = f32_to_bf16(silu_f(acc[mt][2]) * acc[mt][3]);
-    } else if (n0 + 3 < a.N) {
-      uint16_t* yp = a.y + (size_t)m * a.ldy + n0;
-      float o[4] = {acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]};
-      if (a.epi == EPI_RESIDUAL) {
-        const uint2 old = *reinterpret_cast<const uint2*>(yp);
-        o[0] += bf16_to_f32((uint16_t)(old.x & 0xFFFFu));
-        o[1] += bf16_to_f32((uint16_t)(old.x >> 16));
-        o[2] += bf16_to_f32((uint16_t)(old.y & 0xFFFFu));
-        o[3] += bf16_to_f32((uint16_t)(old.y >> 16));
-      }
-      uint2 pk;
-      pk.x = (uint32_t)f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
-      pk.y = (uint32_t)f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
-      *reinterpret_cast<uint2*>(yp) = pk;
-    } else {
-      for (int v = 0; v < 4; ++v) {
-        const int n = n0 + v;
-        if (n >= a.N) break;
-        float o = acc[mt][v];
-        if (a.epi == EPI_RESIDUAL) o += bf16_to_f32(a.y[(size_t)m * a.ldy + n]);
-        a.y[(size_t)m * a.ldy + n] = f32_to_bf16(o);
-      }
+    for (int step = 0; step < U; ++step) {
+      const int uu = u0 + step * G;
+      if (wave == (step & 3) && uu < nunits) arrive<MT>(a, uu / ks, lane, c, r16);
     }
   }
 }
 
-size_t gemv_lds_bytes(int MT, int gpr) {
-  return (size_t)(16 * MT + 1) * xrow_stride(gpr) * 2 + (size_t)(16 * MT + 1) * gpr * 2 * 4 +
-         (size_t)GEMV_WAVES * MT * 64 * 4 * 4;
+// K-range plan of a shape for an M class (MT = 1: M <= 16; MT > 1: M <= 64).  Depends
+// only on (N, K, class): a token's reduction order never changes with the number of
+// tokens in its class, nor with the grid the launch gets.
+void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit) {
+  const int Mr = MT == 1 ? 16 : 64;
+  int d = 3;
+  while (d > 1 && gemv_lds_bytes(Mr, GEMV_WAVES * d, MT) > (size_t)GEMV_LDS_LIMIT) --d;
+  *kr = std::min(L.GP, GEMV_WAVES * d);
+  *ksplit = (L.GP + *kr - 1) / *kr;
 }
 
-// K-range plan for a shape.  Depends only on (N, K, MT): a token's reduction order
-// never changes with the number of tokens in the same m-tile class.
-void gemv_plan(const QLinear& L, int MT, int* gpr, int* ksplit) {
-  int s = 1;
-  // LDS must hold the K-range for the class's largest M
-  while (gemv_lds_bytes(MT, (L.GP + s - 1) / s) > (size_t)GEMV_LDS_LIMIT) ++s;
-  // at least ~640 blocks (2.5 per CU) and at least 4 group pairs per block
-  while ((long)L.NT * s < 640 && (L.GP + s) / (s + 1) >= 4) ++s;
-  *gpr = (L.GP + s - 1) / s;
-  *ksplit = (L.GP + *gpr - 1) / *gpr;
+static int g_cus = 0;
+
+// resident blocks per CU of one kernel instance at one LDS size (cached)
+template <int MT, int D, int U>
+static int occupancy(size_t lds) {
+  static int cache_lds[8] = {-1, -1, -1, -1, -1, -1, -1, -1}, cache_n[8];
+  for (int i = 0; i < 8; ++i)
+    if (cache_lds[i] == (int)lds) return cache_n[i];
+  int n = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)qgemv_kernel<MT, D, U>, 256, lds) != hipSuccess || n < 1)
+    n = 1;
+  for (int i = 0; i < 8; ++i)
+    if (cache_lds[i] < 0) { cache_lds[i] = (int)lds; cache_n[i] = n; break; }
+  return n;
+}
+
+template <int MT, int D, int U>
+static void launch_mdu(const GemvArgs& a, size_t lds, hipStream_t st) {
+  const int nunits = a.NT * a.ksplit;
+  int G = (nunits + U - 1) / U;
+  G += (a.ksplit - G % a.ksplit) % a.ksplit;  // a block's K-range stays fixed: G % ksplit == 0
+  hipLaunchKernelGGL((qgemv_kernel<MT, D, U>), dim3(G), dim3(256), lds, st, a);
+}
+
+// Units per block: enough that one round of resident blocks covers the launch, up to 4.
+template <int MT, int D>
+static void launch_md(const GemvArgs& a, size_t lds, hipStream_t st) {
+  const int nunits = a.NT * a.ksplit;
+  const int cap = g_cus * occupancy<MT, D, 1>(lds);
+  const int need = (nunits + cap - 1) / cap;
+  if (need <= 1) launch_mdu<MT, D, 1>(a, lds, st);
+  else if (need == 2) launch_mdu<MT, D, 2>(a, lds, st);
+  else launch_mdu<MT, D, 4>(a, lds, st);
+}
+
+template <int MT>
+static void launch_mt(const GemvArgs& a, int D, size_t lds, hipStream_t st) {
+  switch (D) {
+    case 1: launch_md<MT, 1>(a, lds, st); break;
+    case 2: launch_md<MT, 2>(a, lds, st); break;
+    default: launch_md<MT, 3>(a, lds, st); break;
+  }
 }
 
 int gemv_launch(const GemvArgs& a, int MT, hipStream_t st) {
-  dim3 grid(a.NT, a.ksplit), block(256);
-  const size_t lds = gemv_lds_bytes(MT, a.gpr);
+  if (g_cus == 0) {
+    int dev = 0;
+    MC_HIP(hipGetDevice(&dev));
+    MC_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (g_cus < 1) g_cus = 1;
+  }
+  const int Mr = std::min(a.M, 16 * MT);
+  const size_t lds = gemv_lds_bytes(Mr, a.kr, MT);
   if (lds > (size_t)GEMV_LDS_LIMIT) return fail(MC_E_INVALID, "gemv: K-range exceeds LDS");
-  if (a.M < 1 || a.M > 16 * MT) return fail(MC_E_INVALID, "gemv: M outside the m-tile class");
+  if (a.M < 1 || a.M > 16 * MT || (MT > 1 && a.M <= 16)) return fail(MC_E_INVALID, "gemv: M outside the m-tile class");
+  if (a.K % 64 || a.GP != (a.K + 127) / 128 || a.NT != (a.N + 15) / 16) return fail(MC_E_INVALID, "gemv: bad shape");
+  if (a.kr < 1 || a.kr > GEMV_WAVES * 3 || a.ksplit != (a.GP + a.kr - 1) / a.kr)
+    return fail(MC_E_INVALID, "gemv: bad K-range plan");
+  if (a.norm_w && (!a.ss_in || a.ss_nt < 1 || a.ss_nt > 256 || a.ss_ld < a.M))
+    return fail(MC_E_INVALID, "gemv: fused norm needs the producer's sums of squares (<= 256 tiles)");
+  if (a.epi == EPI_RESIDUAL && (a.N % 16 || (a.ss_out && a.ss_ld_out < a.M)))
+    return fail(MC_E_INVALID, "gemv: residual epilogue needs N % 16 == 0");
+  const int D = (a.kr + GEMV_WAVES - 1) / GEMV_WAVES;  // group pairs per wave per unit
   switch (MT) {
-    case 1: hipLaunchKernelGGL(qgemv_kernel<1>, grid, block, lds, st, a); break;
-    case 2: hipLaunchKernelGGL(qgemv_kernel<2>, grid, block, lds, st, a); break;
-    case 3: hipLaunchKernelGGL(qgemv_kernel<3>, grid, block, lds, st, a); break;
-    case 4: hipLaunchKernelGGL(qgemv_kernel<4>, grid, block, lds, st, a); break;
+    case 1: launch_mt<1>(a, D, lds, st); break;
+    case 2: launch_mt<2>(a, D, lds, st); break;
+    case 3: launch_mt<3>(a, D, lds, st); break;
+    case 4: launch_mt<4>(a, D, lds, st); break;
     default: return fail(MC_E_INVALID, "gemv: unsupported m-tile count");
   }
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
 
+template <int MT, int D>
+static int setup_md() {
+  const void* fns[] = {(const void*)qgemv_kernel<MT, D, 1>, (const void*)qgemv_kernel<MT, D, 2>,
+                       (const void*)qgemv_kernel<MT, D, 4>};
+  for (const void* f : fns) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
+  return MC_OK;
+}
+
+template <int MT>
+static int setup_mt() {
+  int rc;
+  if ((rc = setup_md<MT, 1>()) || (rc = setup_md<MT, 2>()) || (rc = setup_md<MT, 3>())) return rc;
+  return MC_OK;
+}
+
 int gemv_setup_lds() {
-  MC_HIP(hipFuncSetAttribute((const void*)qgemv_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
-  MC_HIP(hipFuncSetAttribute((const void*)qgemv_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
-  MC_HIP(hipFuncSetAttribute((const void*)qgemv_kernel<3>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
-  MC_HIP(hipFuncSetAttribute((const void*)qgemv_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
+  int rc;
+  if ((rc = setup_mt<1>()) || (rc = setup_mt<2>()) || (rc = setup_mt<3>()) || (rc = setup_mt<4>())) return rc;
   return MC_OK;
 }
 
@@ -291,9 +522,9 @@ __device__ inline size_t tile_word_index(const QLinear& L, int nd, int kw) {
   return (((size_t)t * L.GP + gp) * 64 + lane) * 4 + gi * 2 + am;
 }
 __device__ inline size_t tile_sb_index(const QLinear& L, int nd, int g) {
-  const int t = nd >> 4, r = nd & 15, c = r >> 2, v = r & 3;
+  const int t = nd >> 4, r = nd & 15;
   const int gp = g >> 1, gi = g & 1;
-  return (((size_t)t * L.GP + gp) * 4 + c) * 8 + gi * 4 + v;
+  return (((size_t)t * L.GP + gp) * 16 + r) * 2 + gi;
 }
 
 __global__ void repack_kernel(QLinear L, int row_off, int row_stride, int Nsrc, const uint32_t* wq,

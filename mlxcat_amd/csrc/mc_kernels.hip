@@ -1,5 +1,5 @@
 // mc_kernels.hip -- per-token kernels of the verify forward for gfx950:
-// quantized-embedding gather, RMSNorm, fused q/k-norm + RoPE + KV append, and
+// quantized-embedding gather, fused q/k-norm + RoPE + KV append, and
 // split-KV GQA attention over each row's contiguous K/V (one query block per
 // (row, kv head): the (K+1) verify positions x the GQA group share every key load).
 //
@@ -15,35 +15,48 @@ namespace mc {
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
-// embedding: dequantised row of the tile-layout [V, H] tensor, bf16(fma(s, q, b))
+// embedding: dequantised row of the tile-layout [V, H] tensor, bf16(fma(s, q, b)).
+// One thread per (token, 16 hidden elements); it also writes the 16 elements' sum of
+// squares, the per-tile partial the first layer's fused RMSNorm reduces.
 // ---------------------------------------------------------------------------
-__global__ void embed_kernel(QLinear E, const int32_t* slot_tok, int M, int H, uint16_t* x) {
-  const int per_row = H / 8;
+__global__ void embed_kernel(QLinear E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld) {
+  const int nt = H / 16;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M * per_row) return;
-  const int m = i / per_row, kw = i - m * per_row;
+  if (i >= M * nt) return;
+  const int m = i / nt, tt = i - m * nt;
   int tok = slot_tok[m];
   if (tok < 0 || tok >= E.N) tok = 0;
   const int t = tok >> 4, r = tok & 15;
-  const int g = kw >> 3, w8 = kw & 7, am = w8 >> 2, c = w8 & 3;
-  const int gp = g >> 1, gi = g & 1;
-  const uint32_t word = E.qw[(((size_t)t * E.GP + gp) * 64 + c * 16 + r) * 4 + gi * 2 + am];
-  const uint32_t sbw = E.sb[(((size_t)t * E.GP + gp) * 4 + (r >> 2)) * 8 + gi * 4 + (r & 3)];
-  const float s = bf16_to_f32((uint16_t)(sbw & 0xFFFFu)), b = bf16_to_f32((uint16_t)(sbw >> 16));
-  uint32_t out[4];
+  float q = 0.f;
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const float q0 = (float)((word >> (4 * p)) & 0xFu);          // element 2p
-    const float q1 = (float)((word >> (16 + 4 * p)) & 0xFu);     // element 2p + 1
-    out[p] = (uint32_t)f32_to_bf16(__builtin_fmaf(s, q0, b)) | ((uint32_t)f32_to_bf16(__builtin_fmaf(s, q1, b)) << 16);
+  for (int half = 0; half < 2; ++half) {
+    const int kw = tt * 2 + half;
+    const int g = kw >> 3, w8 = kw & 7, am = w8 >> 2, c = w8 & 3;
+    const int gp = g >> 1, gi = g & 1;
+    const uint32_t word = E.qw[(((size_t)t * E.GP + gp) * 64 + c * 16 + r) * 4 + gi * 2 + am];
+    const uint32_t sbw = E.sb[(((size_t)t * E.GP + gp) * 16 + r) * 2 + gi];
+    const float s = bf16_to_f32((uint16_t)(sbw & 0xFFFFu)), b = bf16_to_f32((uint16_t)(sbw >> 16));
+    uint32_t out[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint16_t h0 = f32_to_bf16(__builtin_fmaf(s, (float)((word >> (4 * p)) & 0xFu), b));       // element 2p
+      const uint16_t h1 = f32_to_bf16(__builtin_fmaf(s, (float)((word >> (16 + 4 * p)) & 0xFu), b));  // element 2p + 1
+      const float v0 = bf16_to_f32(h0), v1 = bf16_to_f32(h1);
+      q += v0 * v0;
+      q += v1 * v1;
+      out[p] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    }
+    u32x4 v = {out[0], out[1], out[2], out[3]};
+    *reinterpret_cast<u32x4*>(x + (size_t)m * H + kw * 8) = v;
   }
-  u32x4 v = {out[0], out[1], out[2], out[3]};
-  *reinterpret_cast<u32x4*>(x + (size_t)m * H + kw * 8) = v;
+  ssq[(size_t)tt * ss_ld + m] = q;
 }
 
-int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, hipStream_t st) {
-  const int total = M * (H / 8);
-  hipLaunchKernelGGL(embed_kernel, dim3((total + 255) / 256), dim3(256), 0, st, E, slot_tok, M, H, x);
+int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld,
+                 hipStream_t st) {
+  if (H % 16) return fail(MC_E_INVALID, "embed: hidden size must be a multiple of 16");
+  const int total = M * (H / 16);
+  hipLaunchKernelGGL(embed_kernel, dim3((total + 255) / 256), dim3(256), 0, st, E, slot_tok, M, H, x, ssq, ss_ld);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
@@ -63,35 +76,7 @@ __device__ inline float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm: one 256-thread block per token
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const uint16_t* w, int H, float eps,
-                                                      uint16_t* y) {
-  __shared__ float red[4];
-  const int m = blockIdx.x, tid = threadIdx.x;
-  const uint16_t* xr = x + (size_t)m * H;
-  float ss = 0.f;
-  for (int i = tid; i < H; i += 256) {
-    const float v = bf16_to_f32(xr[i]);
-    ss += v * v;
-  }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  const float r = 1.0f / sqrtf(tot / (float)H + eps);
-  for (int i = tid; i < H; i += 256)
-    y[(size_t)m * H + i] = f32_to_bf16((bf16_to_f32(xr[i]) * r) * bf16_to_f32(w[i]));
-}
-
-int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, float eps, uint16_t* y, hipStream_t st) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, st, x, w, H, eps, y);
-  MC_HIP(hipGetLastError());
-  return MC_OK;
-}
-
-// ---------------------------------------------------------------------------
-// q/k RMSNorm (Qwen3) + rotate-half RoPE + KV append.  One block per slot, one
+// q/k RMSNorm (Qwen3) + rotate-half RoPE + KV append.  Grid (slot, head / 4), one
 // wave per head; lane i handles the rotation pair (i, i + d/2) for d = 128.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) qk_rope_append_kernel(const uint16_t* qkv, const uint16_t* q_norm,
@@ -107,13 +92,15 @@ __global__ void __launch_bounds__(256) qk_rope_append_kernel(const uint16_t* qkv
   const int ntot = nq + 2 * nkv;
   const int Nqkv = ntot * d;
   const uint16_t* src = qkv + (size_t)m * Nqkv;
-  for (int hh = wave; hh < ntot; hh += 4) {
+  {
+    const int hh = blockIdx.y * 4 + wave;  // one wave per head
+    if (hh >= ntot) return;
     const uint16_t* hp = src + (size_t)hh * d;
     if (hh >= nq + nkv) {  // V head: copy into the cache
       const int h = hh - nq - nkv;
       uint16_t* dst = kv.v + (((size_t)row * nkv + h) * kv.cap + pos) * d;
       for (int i = lane; i < d; i += 64) dst[i] = hp[i];
-      continue;
+      return;
     }
     const bool is_q = hh < nq;
     const uint16_t* nw = is_q ? q_norm : k_norm;
@@ -153,127 +140,181 @@ int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uin
                           const float* rope_sin, int M, int nq, int nkv, int d, float eps, const int32_t* slot_row,
                           const int32_t* slot_pos, KVLayer kv, uint16_t* q_out, hipStream_t st) {
   if (d > 128 || (d & 1)) return fail(MC_E_INVALID, "head_dim must be even and <= 128");
-  hipLaunchKernelGGL(qk_rope_append_kernel, dim3(M), dim3(256), 0, st, qkv, q_norm, k_norm, rope_cos, rope_sin, nq,
-                     nkv, d, eps, slot_row, slot_pos, kv, q_out);
+  hipLaunchKernelGGL(qk_rope_append_kernel, dim3(M, (nq + 2 * nkv + 3) / 4), dim3(256), 0, st, qkv, q_norm, k_norm,
+                     rope_cos, rope_sin, nq, nkv, d, eps, slot_row, slot_pos, kv, q_out);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
 
 // ---------------------------------------------------------------------------
-// split-KV attention.  Grid (R * nkv, nchunk, qtiles); block 256.  A block loads a
-// 64-key chunk of one (row, kv head) once and scores it against up to 16 queries
-// (verify positions x GQA group), producing per-query partial (max, sum, o[d]).
-// The combine pass merges chunks 0..nc-1 in order, so a query's result depends
-// only on its own position and keys.
+// split-KV attention on the matrix cores.  Grid (R * nkv, nchunk); block 256 = 4 waves.
+// A block stages one 64-key chunk of one (row, kv head) in LDS once -- K as [key][d],
+// V transposed to [d][key] -- and every query of the row that shares the kv head (the
+// verify positions x the GQA group) is scored against it: wave w takes query tiles
+// w, w + 4, ... of 16 queries.  Per tile:
+//   S = Q K^T   4 key blocks x 4 d-steps of v_mfma_f32_16x16x32_bf16,
+//   causal mask by absolute position, row max / sum over the chunk,
+//   O = P V     8 d blocks x 2 key-steps, P split into bf16 hi + lo parts,
+// and the partial (max, sum, O[d]) is written for the combine pass, which merges the
+// chunks in order: a query's result depends only on its own position and keys.
 // ---------------------------------------------------------------------------
-constexpr int KROW = 128 + 2;  // LDS row stride (bf16) for K / V chunks
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int KS_STRIDE = 128 + 8;        // LDS row stride (bf16) of K [key][d]
+constexpr int VT_STRIDE = ATTN_CHUNK + 8; // LDS row stride (bf16) of V^T [d][key]
+constexpr int PL_STRIDE = ATTN_CHUNK + 8; // LDS row stride (bf16) of P [q][key] (hi and lo parts)
 
 __global__ void __launch_bounds__(256) attn_partial_kernel(const uint16_t* q, KVLayer kv, SlotView sv, int nq,
                                                            int nkv, int d, float scale, AttnWork w) {
-  __shared__ uint16_t ks[ATTN_CHUNK * KROW];
-  __shared__ uint16_t vs[ATTN_CHUNK * KROW];
-  __shared__ float qs[ATTN_QTILE * 128];
-  __shared__ float ps[ATTN_QTILE * ATTN_CHUNK];
-  __shared__ float pm[ATTN_QTILE], pl[ATTN_QTILE];
+  __shared__ __align__(16) uint16_t ks[ATTN_CHUNK * KS_STRIDE];
+  __shared__ __align__(16) uint16_t vt[128 * VT_STRIDE];
+  __shared__ __align__(16) uint16_t pl[4 * 2 * 16 * PL_STRIDE];
 
   const int G = nq / nkv;
   const int r = blockIdx.x / nkv, kh = blockIdx.x % nkv;
-  const int chunk = blockIdx.y, qt = blockIdx.z;
+  const int chunk = blockIdx.y;
   const int nv = sv.n_valid[r];
   const int nqry = nv * G;
-  if (qt * ATTN_QTILE >= nqry) return;
+  if (nqry == 0) return;
   const int base = sv.qbase[r];
   const int kend = base + nv;  // keys visible to the last query
   const int k0 = chunk * ATTN_CHUNK;
   if (k0 >= kend) return;
   const int nk = min(ATTN_CHUNK, kend - k0);
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane >> 4, r16 = lane & 15;
   const int slot0 = sv.row_slot0[r];
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
 
-  // stage K, V chunk
+  // ---- stage the chunk: 16-byte loads, K row-major, V transposed; keys >= nk are zero ----
   const uint16_t* kbase = kv.k + (((size_t)r * nkv + kh) * kv.cap + k0) * d;
   const uint16_t* vbase = kv.v + (((size_t)r * nkv + kh) * kv.cap + k0) * d;
-  for (int i = tid; i < nk * (d / 2); i += 256) {
-    const int key = i / (d / 2), e = (i - key * (d / 2)) * 2;
-    const uint32_t kk = *reinterpret_cast<const uint32_t*>(kbase + (size_t)key * d + e);
-    const uint32_t vv = *reinterpret_cast<const uint32_t*>(vbase + (size_t)key * d + e);
-    *reinterpret_cast<uint32_t*>(ks + key * KROW + e) = kk;
-    *reinterpret_cast<uint32_t*>(vs + key * KROW + e) = vv;
+  const int cpk = d / 8;  // 16-byte chunks per key row
+  for (int i = tid; i < ATTN_CHUNK * cpk; i += 256) {
+    const int key = i / cpk, e = (i - key * cpk) * 8;
+    u4 kk = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+    if (key < nk) {
+      kk = *reinterpret_cast<const u4*>(kbase + (size_t)key * d + e);
+      vv = *reinterpret_cast<const u4*>(vbase + (size_t)key * d + e);
+    }
+    *reinterpret_cast<u4*>(ks + key * KS_STRIDE + e) = kk;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      vt[(e + 2 * h) * VT_STRIDE + key] = (uint16_t)(vv[h] & 0xFFFFu);
+      vt[(e + 2 * h + 1) * VT_STRIDE + key] = (uint16_t)(vv[h] >> 16);
+    }
   }
-  // stage queries of this tile
-  for (int i = tid; i < ATTN_QTILE * d; i += 256) {
-    const int qi = i / d, e = i - qi * d;
-    const int gq = qt * ATTN_QTILE + qi;
-    float v = 0.f;
-    if (gq < nqry) {
-      const int j = gq / G, gh = gq - j * G;
-      v = bf16_to_f32(q[(size_t)(slot0 + j) * nq * d + (size_t)(kh * G + gh) * d + e]);
-    }
-    qs[qi * 128 + e] = v;
-  }
-  __syncthreads();
-
-  // scores: thread -> query qi = tid / 16, keys (tid % 16) + 16 i
-  {
-    const int qi = tid >> 4, kl = tid & 15;
-    const int gq = qt * ATTN_QTILE + qi;
-    const int qpos = (gq < nqry) ? base + gq / G : -1;
-    float sc[ATTN_CHUNK / 16];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; ++i) {
-      const int key = kl + 16 * i;
-      float s = -INFINITY;
-      if (key < nk && k0 + key <= qpos) {
-        float a0 = 0.f, a1 = 0.f;
-        for (int e = 0; e < d; e += 2) {
-          a0 += qs[qi * 128 + e] * bf16_to_f32(ks[key * KROW + e]);
-          a1 += qs[qi * 128 + e + 1] * bf16_to_f32(ks[key * KROW + e + 1]);
-        }
-        s = (a0 + a1) * scale;
-      }
-      sc[i] = s;
-      mx = fmaxf(mx, s);
-    }
-    // max / sum over the 16 lanes that share this query (lanes qi*16 .. qi*16+15)
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; ++i) {
-      const float p = (sc[i] == -INFINITY) ? 0.f : __expf(sc[i] - mx);
-      ps[qi * ATTN_CHUNK + kl + 16 * i] = p;
-      l += p;
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
-    if (kl == 0) {
-      pm[qi] = mx;
-      pl[qi] = l;
-    }
+  // d < 128: zero the unused d rows of V^T and d columns of K so the MFMA steps see zeros
+  for (int i = tid; i < (128 - d) * ATTN_CHUNK; i += 256) {
+    const int e = d + i / ATTN_CHUNK, key = i % ATTN_CHUNK;
+    vt[e * VT_STRIDE + key] = 0;
+    ks[key * KS_STRIDE + e] = 0;
   }
   __syncthreads();
 
-  // o[qi][e] = sum_key p[qi][key] v[key][e]; thread -> qi = tid / 16, e = (tid % 16) + 16 i
-  {
-    const int qi = tid >> 4, el = tid & 15;
-    const int gq = qt * ATTN_QTILE + qi;
-    if (gq < nqry) {
-      const int j = gq / G, gh = gq - j * G;
-      const int slot = slot0 + j;
-      const int h = kh * G + gh;
-      float* po = w.part_o + (((size_t)slot * nq + h) * w.nchunk + chunk) * d;
-      for (int e = el; e < d; e += 16) {
-        float a = 0.f;
-        for (int key = 0; key < nk; ++key) a += ps[qi * ATTN_CHUNK + key] * bf16_to_f32(vs[key * KROW + e]);
-        po[e] = a;
+  const int nqt = (nqry + 15) / 16;
+  uint16_t* pw = pl + wave * 2 * 16 * PL_STRIDE;  // [hi | lo][16][PL_STRIDE]
+  const bf16x8_t zero8 = __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
+  for (int qt = wave; qt < nqt; qt += 4) {
+    // A operand: query qt*16 + r16, d = 32s + 8c .. +7
+    const int qa = qt * 16 + r16;
+    bf16x8_t qa_v[4];
+    if (qa < nqry) {
+      const int j = qa / G, gh = qa - j * G;
+      const uint16_t* qp = q + (size_t)(slot0 + j) * nq * d + (size_t)(kh * G + gh) * d;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        qa_v[s4] = (32 * s4 + 8 * c < d) ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * s4 + 8 * c) : zero8;
+    } else {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) qa_v[s4] = zero8;
+    }
+    // S[q = 4c + v][key = 16 kb + r16]
+    f32x4_t sc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const bf16x8_t kb_v = *reinterpret_cast<const bf16x8_t*>(ks + (kb * 16 + r16) * KS_STRIDE + 32 * s4 + 8 * c);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_v[s4], kb_v, acc, 0, 0, 0);
       }
-      if (el == 0) {
+      sc[kb] = acc;
+    }
+    // mask, row max / sum over the chunk (rows 4c + v live in the 16 lanes of group c)
+    float mx[4], lsum[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int qi = qt * 16 + 4 * c + v;
+      const int qpos = qi < nqry ? base + qi / G : -1;
+      float m = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const int key = kb * 16 + r16;
+        const bool ok = key < nk && k0 + key <= qpos;
+        const float s = ok ? sc[kb][v] * scale : -INFINITY;
+        sc[kb][v] = s;
+        m = fmaxf(m, s);
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+      float l = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        // p = hi + lo exactly to ~2^-16: two bf16 MFMA operands keep P V near fp32
+        const float p = (sc[kb][v] == -INFINITY) ? 0.f : __expf(sc[kb][v] - m);
+        const uint16_t ph = f32_to_bf16(p);
+        const uint16_t plo = f32_to_bf16(p - bf16_to_f32(ph));
+        pw[(4 * c + v) * PL_STRIDE + kb * 16 + r16] = ph;
+        pw[(16 + 4 * c + v) * PL_STRIDE + kb * 16 + r16] = plo;
+        l += p;
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
+      mx[v] = m;
+      lsum[v] = l;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P writes are in LDS
+    __builtin_amdgcn_wave_barrier();
+    // O[q = 4c + v][d = 16 db + r16] = sum_key P[q][key] V[key][d]
+    bf16x8_t pa[2], pb2[2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      pa[k2] = *reinterpret_cast<const bf16x8_t*>(pw + r16 * PL_STRIDE + 32 * k2 + 8 * c);
+      pb2[k2] = *reinterpret_cast<const bf16x8_t*>(pw + (16 + r16) * PL_STRIDE + 32 * k2 + 8 * c);
+    }
+    const int nd16 = d / 16;
+    for (int db = 0; db < nd16; ++db) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const bf16x8_t vb = *reinterpret_cast<const bf16x8_t*>(vt + (db * 16 + r16) * VT_STRIDE + 32 * k2 + 8 * c);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[k2], vb, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb2[k2], vb, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int qi = qt * 16 + 4 * c + v;
+        if (qi >= nqry) continue;
+        const int j = qi / G, gh = qi - j * G;
+        const int slot = slot0 + j, h = kh * G + gh;
+        w.part_o[(((size_t)slot * nq + h) * w.nchunk + chunk) * d + db * 16 + r16] = acc[v];
+      }
+    }
+    if (r16 == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int qi = qt * 16 + 4 * c + v;
+        if (qi >= nqry) continue;
+        const int j = qi / G, gh = qi - j * G;
+        const int slot = slot0 + j, h = kh * G + gh;
         float* pml = w.part_ml + (((size_t)slot * nq + h) * w.nchunk + chunk) * 2;
-        pml[0] = pm[qi];
-        pml[1] = pl[qi];
+        pml[0] = mx[v];
+        pml[1] = lsum[v];
       }
     }
+    __builtin_amdgcn_wave_barrier();  // P of this tile is consumed before the next tile overwrites it
   }
 }
 
@@ -304,12 +345,10 @@ __global__ void attn_combine_kernel(SlotView sv, int nq, int d, AttnWork w, uint
 
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
                      int M, const AttnWork& w, uint16_t* att, hipStream_t st) {
-  if (d > 128) return fail(MC_E_INVALID, "attention: head_dim > 128");
-  const int G = nq / nkv;
-  const int qtiles = (max_q * G + ATTN_QTILE - 1) / ATTN_QTILE;
+  if (d > 128 || d % 16) return fail(MC_E_INVALID, "attention: head_dim must be a multiple of 16 and <= 128");
+  (void)max_q;
   const float scale = 1.0f / sqrtf((float)d);
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(R * nkv, w.nchunk, qtiles), dim3(256), 0, st, q, kv, sv, nq, nkv, d,
-                     scale, w);
+  hipLaunchKernelGGL(attn_partial_kernel, dim3(R * nkv, w.nchunk), dim3(256), 0, st, q, kv, sv, nq, nkv, d, scale, w);
   MC_HIP(hipGetLastError());
   hipLaunchKernelGGL(attn_combine_kernel, dim3(M, nq), dim3(128), 0, st, sv, nq, d, w, att);
   MC_HIP(hipGetLastError());

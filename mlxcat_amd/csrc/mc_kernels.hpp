@@ -1,5 +1,5 @@
 // mc_kernels.hpp -- launch interface of the per-token kernels of the verify forward
-// (embedding, RMSNorm, q/k-norm + RoPE + KV append, split-KV GQA attention) and the
+// (embedding, q/k-norm + RoPE + KV append, split-KV GQA attention) and the
 // step kernels (n-gram proposer, acceptance, commit).
 #pragma once
 #include "mc_common.hpp"
@@ -24,8 +24,9 @@ struct KVLayer {
   int cap;
 };
 
-int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, hipStream_t st);
-int launch_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, float eps, uint16_t* y, hipStream_t st);
+// x[m][:] = embedding row of slot_tok[m]; ssq[t * ss_ld + m] = sum of squares of x[m][16t : 16t + 16]
+int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld,
+                 hipStream_t st);
 // qkv [M][(nq + 2 nkv) d] -> q [M][nq d] (normed + rotated), K/V cache append for valid slots
 int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm, const float* rope_cos,
                           const float* rope_sin, int M, int nq, int nkv, int d, float eps, const int32_t* slot_row,
@@ -37,7 +38,6 @@ struct AttnWork {
   int nchunk;      // ceil(cap / ATTN_CHUNK)
 };
 constexpr int ATTN_CHUNK = 64;
-constexpr int ATTN_QTILE = 16;
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
                      int M, const AttnWork& w, uint16_t* att, hipStream_t st);
 

