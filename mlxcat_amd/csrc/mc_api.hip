@@ -344,7 +344,8 @@ struct mc_batch {
            *logits = nullptr;
   float* gemv_part = nullptr;
   unsigned* gemv_cnt = nullptr;
-  float* ssq = nullptr;  // [hidden / 16][Mmax]: per-tile sums of squares of the residual stream
+  float* ssq = nullptr;  // [Mmax][hidden / 16]: per-tile sums of squares of the residual stream
+  unsigned long long* amax = nullptr;  // [Mmax][vocab tiles]: greedy argmax partials of the head
   AttnWork aw{};
   StepState s;
   void* scratch = nullptr;  // one allocation for the small StepState arrays
@@ -374,7 +375,7 @@ static void batch_free(mc_batch* b) {
   if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
-                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
+                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -464,7 +465,8 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     for (auto& L : m->layers) { acc_plan(L.qkv); acc_plan(L.o); acc_plan(L.gateup); acc_plan(L.down); }
     acc_plan(m->head());
     if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt)) ||
-        (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M))) {
+        (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M)) ||
+        (rc = dev_zero(&b->amax, (size_t)M * m->head().NT))) {
       batch_free(b);
       return rc;
     }
@@ -506,6 +508,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   s.qbase = I32(o_qb); s.scan_tok = I32(o_sct); s.scan_acc = I32(o_sca); s.scan_res = I32(o_scr);
   s.forced = I32(o_forced); s.out_tok = I32(o_otok); s.out_cnt = I32(o_ocnt); s.out_fin = I32(o_ofin);
   s.stats = reinterpret_cast<unsigned long long*>(base + o_stats);
+  if (!m->fake) { s.amax = b->amax; s.amax_nt = m->head().NT; }
   // forced = -1 (none), reject = -1
   {
     std::vector<int32_t> neg(R, -1);
@@ -540,12 +543,14 @@ static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
   return MC_OK;
 }
 
-// One linear over M tokens, in launches of at most 64.  norm_w != NULL fuses the
-// RMSNorm of the input rows (their sums of squares are the per-tile partials in b->ssq);
-// EPI_RESIDUAL writes the new rows' partials to b->ssq for the next norm.
-static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, const uint16_t* norm_w, float eps,
-                    uint16_t* y, int ldy, int M, int epi, int ss_m0 = 0) {
-  const int H = b->m->cfg.hidden;
+// One linear over M tokens, in launches of at most 64.  norm_w: the input rows are the
+// residual stream b->x, RMS-normalised with these weights inside the linear from the
+// per-tile sums of squares in b->ssq (rows ss_m0 ...).  EPI_RESIDUAL writes the new rows'
+// sums of squares to b->ssq.
+static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, const uint16_t* norm_w, uint16_t* y,
+                    int ldy, int M, int epi, int ss_m0 = 0, unsigned long long* amax = nullptr) {
+  const auto& c = b->m->cfg;
+  const int H = c.hidden;
   for (int m0 = 0; m0 < M; m0 += 64) {
     const int mc = std::min(64, M - m0);
     const int MT = (mc + 15) / 16;
@@ -553,14 +558,17 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
     a.qw = L.qw; a.sb = L.sb;
     a.x = x + (size_t)m0 * ldx; a.ldx = ldx;
     if (norm_w) {
-      a.norm_w = norm_w; a.eps = eps;
-      a.ss_in = b->ssq + ss_m0 + m0; a.ss_nt = H / 16; a.ss_ld = b->Mmax;
+      a.norm_w = norm_w;
+      a.ss_in = b->ssq + (size_t)(ss_m0 + m0) * (H / 16); a.ss_nt = H / 16; a.ss_ld = H / 16; a.eps = c.rms_eps;
     }
-    if (epi == EPI_RESIDUAL) { a.ss_out = b->ssq + ss_m0 + m0; a.ss_ld_out = b->Mmax; }
+    if (epi == EPI_RESIDUAL) {
+      a.ss_out = b->ssq + (size_t)(ss_m0 + m0) * (H / 16); a.ss_ld_out = H / 16;
+    }
     a.y = y + (size_t)m0 * ldy; a.ldy = ldy;
     a.M = mc; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
     gemv_plan(L, MT, &a.kr, &a.ksplit);
     a.part = b->gemv_part; a.counters = b->gemv_cnt; a.epi = epi;
+    if (amax) a.amax = amax + (size_t)m0 * L.NT;
     size_t e0 = 0;
     int rc = prof_begin(b, &e0);
     if (rc) return rc;
@@ -584,10 +592,11 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
-  if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->ssq, b->Mmax, b->st))) return rc;
+  if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->ssq, H / 16, b->st)))
+    return rc;
   for (int l = 0; l < c.n_layers; ++l) {
     const auto& L = m->layers[(size_t)l];
-    if ((rc = run_gemv(b, L.qkv, b->x, H, L.in_norm, c.rms_eps, b->qkv, Nqkv, M, EPI_STORE))) return rc;
+    if ((rc = run_gemv(b, L.qkv, b->x, H, L.in_norm, b->qkv, Nqkv, M, EPI_STORE))) return rc;
     if ((rc = launch_qk_rope_append(b->qkv, L.q_norm, L.k_norm, b->rope_cos, b->rope_sin, M, nq, nkv, d, c.rms_eps,
                                     s.slot_row, s.slot_pos, b->kv[(size_t)l], b->q, b->st)))
       return rc;
@@ -596,13 +605,13 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
     if ((rc = launch_attention(b->q, b->kv[(size_t)l], sv, b->R, max_q, nq, nkv, d, M, b->aw, b->att, b->st)))
       return rc;
     if ((rc = prof_end(b, e0, 1, 0.0))) return rc;
-    if ((rc = run_gemv(b, L.o, b->att, nq * d, nullptr, 0.f, b->x, H, M, EPI_RESIDUAL))) return rc;
-    if ((rc = run_gemv(b, L.gateup, b->x, H, L.post_norm, c.rms_eps, b->act, I, M, EPI_SWIGLU))) return rc;
-    if ((rc = run_gemv(b, L.down, b->act, I, nullptr, 0.f, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if ((rc = run_gemv(b, L.o, b->att, nq * d, nullptr, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if ((rc = run_gemv(b, L.gateup, b->x, H, L.post_norm, b->act, I, M, EPI_SWIGLU))) return rc;
+    if ((rc = run_gemv(b, L.down, b->act, I, nullptr, b->x, H, M, EPI_RESIDUAL))) return rc;
   }
   if (lgn > 0) {
-    if ((rc = run_gemv(b, m->head(), b->x + (size_t)lg0 * H, H, m->final_norm, c.rms_eps, b->logits + (size_t)lg0 * c.vocab,
-                       c.vocab, lgn, EPI_STORE, lg0)))
+    if ((rc = run_gemv(b, m->head(), b->x + (size_t)lg0 * H, H, m->final_norm, b->logits + (size_t)lg0 * c.vocab, c.vocab, lgn,
+                       EPI_STORE, lg0, b->amax + (size_t)lg0 * m->head().NT)))
       return rc;
   }
   return MC_OK;

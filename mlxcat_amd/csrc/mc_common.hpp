@@ -29,11 +29,23 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line);
 __host__ __device__ inline float bf16_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
+// Round to nearest even.  On the device this is gfx950's v_cvt_pk_bf16_f32; the host
+// restatement gives the same bits for every non-NaN input.
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
   uint32_t r = u + 0x7FFFu + ((u >> 16) & 1u);
   return (uint16_t)(r >> 16);
+#endif
+}
+
+// order-preserving 16-bit key of a bf16 value, with -0 folded into +0
+__host__ __device__ inline uint32_t bf16_order_key(uint16_t h) {
+  if ((h & 0x7FFFu) == 0) h = 0;
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xFFFFu) : (uint32_t)(h | 0x8000u);
 }
 
 // splitmix64 finalizer (Steele, Lea, Flood 2014)

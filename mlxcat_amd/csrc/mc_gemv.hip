@@ -177,9 +177,19 @@ __device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t
         }
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
-        if (live && r16 == 0 && a.ss_out) a.ss_out[(size_t)t * a.ss_ld_out + m] = q;
-      } else if (live && n < a.N) {
-        a.y[(size_t)m * a.ldy + n] = f32_to_bf16(acc[mt][v]);
+        if (live && r16 == 0 && a.ss_out) a.ss_out[(size_t)m * a.ss_ld_out + t] = q;
+      } else {
+        const uint16_t h = f32_to_bf16(acc[mt][v]);
+        if (live && n < a.N) a.y[(size_t)m * a.ldy + n] = h;
+        if (a.amax) {
+          // tile argmax over 16 rows: 32-bit key (value key << 16 | 15 - row), lowest row on ties
+          unsigned key = (live && n < a.N) ? (bf16_order_key(h) << 16) | (unsigned)(15 - r16) : 0u;
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) key = max(key, (unsigned)__shfl_xor((int)key, o));
+          if (live && r16 == 0 && key)
+            a.amax[(size_t)m * a.NT + t] =
+                ((unsigned long long)(key >> 16) << 32) | (0xFFFFFFFFull - (unsigned)(t * 16 + 15 - (int)(key & 15u)));
+        }
       }
     }
   }
@@ -250,8 +260,9 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   const int c = lane >> 4, r16 = lane & 15;
 
   // ---- 1. small loads first (vmcnt retires in order): norm partials and weights, X ----
-  // row scale of the fused RMSNorm: wave w reduces rows w, w + 4, ... over the producer's
-  // per-tile sums of squares, lane l taking tiles l, l + 64, ... (fixed order)
+  // row scale of the fused RMSNorm, r[m] = 1 / sqrt(mean(x^2) + eps): wave w reduces rows
+  // w, w + 4, ... over the producer's per-tile sums of squares, lane l taking tiles
+  // l, l + 64, ... (fixed order)
   constexpr int RW = MT * 4;         // rows per wave, at most
   constexpr int SL = 4;              // producer tiles per lane, at most (ss_nt <= 256)
   float ssv[RW][SL];
@@ -259,9 +270,9 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
-      for (int u = 0; u < SL; ++u) {
-        const int m = wave + GEMV_WAVES * r, tt = lane + 64 * u;
-        ssv[r][u] = (m < Mr && tt < a.ss_nt) ? a.ss_in[(size_t)tt * a.ss_ld + m] : 0.f;
+      for (int q = 0; q < SL; ++q) {
+        const int m = wave + GEMV_WAVES * r, tt = lane + 64 * q;
+        ssv[r][q] = (m < Mr && tt < a.ss_nt) ? a.ss_in[(size_t)m * a.ss_ld + tt] : 0.f;
       }
   }
   constexpr int XCH = 8;             // 16-byte X chunks per thread per pass
@@ -269,21 +280,21 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   u32x4 nw[2];                       // norm weights of the K-range (cpr <= 320 chunks)
   if (a.norm_w) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int k = k0 + (tid + 256 * u) * 8;
-      nw[u] = (u32x4){0u, 0u, 0u, 0u};
-      if (tid + 256 * u < cpr && k < a.K) nw[u] = *reinterpret_cast<const u32x4*>(a.norm_w + k);
+    for (int q = 0; q < 2; ++q) {
+      const int k = k0 + (tid + 256 * q) * 8;
+      nw[q] = (u32x4){0u, 0u, 0u, 0u};
+      if (tid + 256 * q < cpr && k < a.K) nw[q] = *reinterpret_cast<const u32x4*>(a.norm_w + k);
     }
   }
   const int xtotal = Mr * cpr;
   u32x4 xv[XCH];
 #pragma unroll
-  for (int u = 0; u < XCH; ++u) {
-    const int i = tid + 256 * u;
-    xv[u] = (u32x4){0u, 0u, 0u, 0u};
+  for (int q = 0; q < XCH; ++q) {
+    const int i = tid + 256 * q;
+    xv[q] = (u32x4){0u, 0u, 0u, 0u};
     if (i < xtotal) {
       const int m = i / cpr, ch = i - m * cpr;
-      if (k0 + ch * 8 < a.K) xv[u] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
+      if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
     }
   }
 
@@ -292,7 +303,8 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   WBuf<D> wa, wb;
   load_unit<D>(wa, a, min(u, nunits - 1) / ks, gp0, ngp, wave, lane, r16);
 
-  // ---- 3. row scales, then X (normalised) into LDS while the weights are in flight ----
+  // ---- 3. row scales and norm weights, then X (normalised) into LDS while the weights are
+  // in flight ----
   if (a.norm_w) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
@@ -317,6 +329,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
         const int m = i / cpr, ch = i - m * cpr;
         u32x4 v = xv[q];
         if (a.norm_w) {
+          // bf16((x * r) * w): the rounding of a standalone RMSNorm
           const float r = rs[m];
           const u32x4 w = *reinterpret_cast<const u32x4*>(wl + ch * 8);
 #pragma unroll
@@ -327,6 +340,26 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
           }
         }
         *reinterpret_cast<u32x4*>(xl + m * XS + ch * 8) = v;
+      }
+      // group sum of X: the 8 chunks of a 64-wide group sit in 8 consecutive lanes (cpr is
+      // a multiple of 16), reduced in a fixed butterfly order
+      float gs = 0.f;
+      if (i < xtotal) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(xl + (i / cpr) * XS + (i % cpr) * 8);
+        float q0 = 0.f, q1 = 0.f;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          q0 += bf16_to_f32((uint16_t)(v[h] & 0xFFFFu));
+          q1 += bf16_to_f32((uint16_t)(v[h] >> 16));
+        }
+        gs = q0 + q1;
+      }
+      gs += __shfl_xor(gs, 1);
+      gs += __shfl_xor(gs, 2);
+      gs += __shfl_xor(gs, 4);
+      if (i < xtotal && (i & 7) == 0) {
+        const int m = i / cpr, gl = (i % cpr) >> 3;
+        xsum[gl * 16 * MT + m] = gs;
       }
     }
   };
@@ -346,19 +379,10 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0);  // leave no load of this branch pending at the merge
   }
-  lds_barrier();
-  for (int i = tid; i < 16 * MT * ng; i += 256) {
-    const int m = i % (16 * MT), gl = i / (16 * MT);
-    const uint16_t* p = xl + min(m, Mr - 1) * XS + gl * 64;
-    float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 64; k += 4) {
-      q0 += bf16_to_f32(p[k]);
-      q1 += bf16_to_f32(p[k + 1]);
-      q2 += bf16_to_f32(p[k + 2]);
-      q3 += bf16_to_f32(p[k + 3]);
-    }
-    xsum[gl * 16 * MT + m] = (q0 + q1) + (q2 + q3);
+  // token rows Mr .. 16 MT - 1 of xsum: zero (their MFMA columns are finite and never stored)
+  for (int i = tid; i < (16 * MT - Mr) * ng; i += 256) {
+    const int m = Mr + i % (16 * MT - Mr), gl = i / (16 * MT - Mr);
+    xsum[gl * 16 * MT + m] = 0.f;
   }
   lds_barrier();
 
@@ -410,7 +434,8 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
 // tokens in its class, nor with the grid the launch gets.
 void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit) {
   const int Mr = MT == 1 ? 16 : 64;
-  int d = 3;
+  // one K-range when it fits 5 group pairs per wave (no split-K tail), else 3 per wave
+  int d = (MT == 1 && L.GP <= GEMV_WAVES * 5) ? 5 : 3;
   while (d > 1 && gemv_lds_bytes(Mr, GEMV_WAVES * d, MT) > (size_t)GEMV_LDS_LIMIT) --d;
   *kr = std::min(L.GP, GEMV_WAVES * d);
   *ksplit = (L.GP + *kr - 1) / *kr;
@@ -440,23 +465,39 @@ static void launch_mdu(const GemvArgs& a, size_t lds, hipStream_t st) {
   hipLaunchKernelGGL((qgemv_kernel<MT, D, U>), dim3(G), dim3(256), lds, st, a);
 }
 
-// Units per block: enough that one round of resident blocks covers the launch, up to 4.
+// Units per block: enough that one round of resident blocks covers the launch (every
+// block stages its activations once, so fewer, longer-lived blocks amortise that).
 template <int MT, int D>
 static void launch_md(const GemvArgs& a, size_t lds, hipStream_t st) {
   const int nunits = a.NT * a.ksplit;
   const int cap = g_cus * occupancy<MT, D, 1>(lds);
   const int need = (nunits + cap - 1) / cap;
-  if (need <= 1) launch_mdu<MT, D, 1>(a, lds, st);
-  else if (need == 2) launch_mdu<MT, D, 2>(a, lds, st);
-  else launch_mdu<MT, D, 4>(a, lds, st);
+  if (need <= 1) {
+    launch_mdu<MT, D, 1>(a, lds, st);
+  } else if (need == 2) {
+    launch_mdu<MT, D, 2>(a, lds, st);
+  } else if constexpr (MT > 1) {
+    launch_mdu<MT, D, 4>(a, lds, st);
+  } else {
+    if (need <= 4) launch_mdu<MT, D, 4>(a, lds, st);
+    else if (need <= 8) launch_mdu<MT, D, 8>(a, lds, st);
+    else launch_mdu<MT, D, 16>(a, lds, st);
+  }
 }
 
 template <int MT>
 static void launch_mt(const GemvArgs& a, int D, size_t lds, hipStream_t st) {
-  switch (D) {
-    case 1: launch_md<MT, 1>(a, lds, st); break;
-    case 2: launch_md<MT, 2>(a, lds, st); break;
-    default: launch_md<MT, 3>(a, lds, st); break;
+  if constexpr (MT > 1) {  // the large-M classes use at most 2 group pairs per wave (LDS)
+    if (D <= 1) launch_md<MT, 1>(a, lds, st);
+    else launch_md<MT, 2>(a, lds, st);
+  } else {
+    switch (D) {
+      case 1: launch_md<MT, 1>(a, lds, st); break;
+      case 2: launch_md<MT, 2>(a, lds, st); break;
+      case 3: launch_md<MT, 3>(a, lds, st); break;
+      case 4: launch_md<MT, 4>(a, lds, st); break;
+      default: launch_md<MT, 5>(a, lds, st); break;
+    }
   }
 }
 
@@ -472,11 +513,12 @@ int gemv_launch(const GemvArgs& a, int MT, hipStream_t st) {
   if (lds > (size_t)GEMV_LDS_LIMIT) return fail(MC_E_INVALID, "gemv: K-range exceeds LDS");
   if (a.M < 1 || a.M > 16 * MT || (MT > 1 && a.M <= 16)) return fail(MC_E_INVALID, "gemv: M outside the m-tile class");
   if (a.K % 64 || a.GP != (a.K + 127) / 128 || a.NT != (a.N + 15) / 16) return fail(MC_E_INVALID, "gemv: bad shape");
-  if (a.kr < 1 || a.kr > GEMV_WAVES * 3 || a.ksplit != (a.GP + a.kr - 1) / a.kr)
+  if (a.kr < 1 || a.kr > GEMV_WAVES * 5 || a.ksplit != (a.GP + a.kr - 1) / a.kr)
     return fail(MC_E_INVALID, "gemv: bad K-range plan");
-  if (a.norm_w && (!a.ss_in || a.ss_nt < 1 || a.ss_nt > 256 || a.ss_ld < a.M))
+  if (a.norm_w && (!a.ss_in || a.ss_nt < 1 || a.ss_nt > 256 || a.ss_ld < a.ss_nt))
     return fail(MC_E_INVALID, "gemv: fused norm needs the producer's sums of squares (<= 256 tiles)");
-  if (a.epi == EPI_RESIDUAL && (a.N % 16 || (a.ss_out && a.ss_ld_out < a.M)))
+  if (a.amax && a.epi != EPI_STORE) return fail(MC_E_INVALID, "gemv: argmax partials need the store epilogue");
+  if (a.epi == EPI_RESIDUAL && (a.N % 16 || (a.ss_out && a.ss_ld_out < a.NT)))
     return fail(MC_E_INVALID, "gemv: residual epilogue needs N % 16 == 0");
   const int D = (a.kr + GEMV_WAVES - 1) / GEMV_WAVES;  // group pairs per wave per unit
   switch (MT) {
@@ -495,13 +537,20 @@ static int setup_md() {
   const void* fns[] = {(const void*)qgemv_kernel<MT, D, 1>, (const void*)qgemv_kernel<MT, D, 2>,
                        (const void*)qgemv_kernel<MT, D, 4>};
   for (const void* f : fns) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
+  if constexpr (MT == 1) {
+    const void* more[] = {(const void*)qgemv_kernel<MT, D, 8>, (const void*)qgemv_kernel<MT, D, 16>};
+    for (const void* f : more) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
+  }
   return MC_OK;
 }
 
 template <int MT>
 static int setup_mt() {
   int rc;
-  if ((rc = setup_md<MT, 1>()) || (rc = setup_md<MT, 2>()) || (rc = setup_md<MT, 3>())) return rc;
+  if ((rc = setup_md<MT, 1>()) || (rc = setup_md<MT, 2>())) return rc;
+  if constexpr (MT == 1) {
+    if ((rc = setup_md<MT, 3>()) || (rc = setup_md<MT, 4>()) || (rc = setup_md<MT, 5>())) return rc;
+  }
   return MC_OK;
 }
 

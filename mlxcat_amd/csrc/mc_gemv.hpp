@@ -11,12 +11,16 @@ struct GemvArgs {
   const uint32_t* sb = nullptr;      // tile-layout scale|bias
   const uint16_t* x = nullptr;       // [M][ldx] bf16
   int ldx = 0;
-  const uint16_t* norm_w = nullptr;  // non-null: the input is RMSNorm(x) * norm_w over the full row,
-  float eps = 0.f;                   //   whose sum of squares is sum_t ss_in[t * ss_ld + m], t < ss_nt
+  // RMSNorm fused into the consumer: with norm_w set the input rows are the raw residual
+  // stream x and each block stages bf16((x[m][k] * r[m]) * norm_w[k]) for its K-range, with
+  // r[m] = 1 / sqrt(sum_t ss_in[m * ss_ld + t] / K + eps) from the producer's per-tile sums of
+  // squares -- the rounding point of a standalone RMSNorm followed by the linear
+  const uint16_t* norm_w = nullptr;  // [K] bf16 (NULL: no norm)
   const float* ss_in = nullptr;
   int ss_nt = 0, ss_ld = 0;
-  float* ss_out = nullptr;           // EPI_RESIDUAL: per-tile sums of squares of the new rows,
-  int ss_ld_out = 0;                 //   ss_out[t * ss_ld_out + m] (NULL = skip)
+  float eps = 0.f;
+  float* ss_out = nullptr;           // EPI_RESIDUAL: ss_out[m * ss_ld_out + t] of the new rows (NULL = skip)
+  int ss_ld_out = 0;
   uint16_t* y = nullptr;             // [M][ldy] bf16 (EPI_RESIDUAL: read-modify-write)
   int ldy = 0;
   int M = 0, N = 0, K = 0, NT = 0, GP = 0;
@@ -25,6 +29,10 @@ struct GemvArgs {
   unsigned* counters = nullptr;      // [NT], zero at rest
   int epi = EPI_STORE;
   uint32_t dq_mask = 0x000F000Fu, dq_magic = 0x43004300u;  // nibble-pair -> bf16 (128 + q) constants
+  // EPI_STORE only, non-null: amax[m * NT + t] = max over the tile's 16 rows of
+  // (order-preserving key of the stored bf16 value) << 32 | (0xFFFFFFFF - row): the tile's
+  // greedy argmax, lowest row on ties
+  unsigned long long* amax = nullptr;
 };
 
 size_t gemv_lds_bytes(int Mr, int kr, int MT);

@@ -17,7 +17,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------
 // embedding: dequantised row of the tile-layout [V, H] tensor, bf16(fma(s, q, b)).
 // One thread per (token, 16 hidden elements); it also writes the 16 elements' sum of
-// squares, the per-tile partial the first layer's fused RMSNorm reduces.
+// squares (ssq[m * ss_ld + t]): the RMSNorm partials of the first linear's input.
 // ---------------------------------------------------------------------------
 __global__ void embed_kernel(QLinear E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld) {
   const int nt = H / 16;
@@ -46,10 +46,10 @@ __global__ void embed_kernel(QLinear E, const int32_t* slot_tok, int M, int H, u
       q += v1 * v1;
       out[p] = (uint32_t)h0 | ((uint32_t)h1 << 16);
     }
-    u32x4 v = {out[0], out[1], out[2], out[3]};
+    const u32x4 v = {out[0], out[1], out[2], out[3]};
     *reinterpret_cast<u32x4*>(x + (size_t)m * H + kw * 8) = v;
   }
-  ssq[(size_t)tt * ss_ld + m] = q;
+  ssq[(size_t)m * ss_ld + tt] = q;
 }
 
 int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld,
@@ -318,29 +318,54 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const uint16_t* q, KV
   }
 }
 
-// one block (d threads) per (slot, head): merge chunks 0..nc-1 in order
-__global__ void attn_combine_kernel(SlotView sv, int nq, int d, AttnWork w, uint16_t* att) {
-  const int m = blockIdx.x, h = blockIdx.y, e = threadIdx.x;
-  const int row = sv.slot_row[m];
+// One wave per (slot, head): merge the chunk partials 0..nc-1 in chunk order with a running
+// max (each lane owns d/64 output elements); loads of 8 chunks are in flight at a time.
+__global__ void __launch_bounds__(256) attn_combine_kernel(SlotView sv, int M, int nq, int d, AttnWork w, uint16_t* att) {
+  const int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  if (wid >= M * nq) return;
+  const int m = wid / nq, h = wid - m * nq;
   uint16_t* out = att + ((size_t)m * nq + h) * d;
+  const int row = sv.slot_row[m];
+  const int e0 = lane * 2;  // d <= 128: lane owns elements e0, e0 + 1
   if (row < 0) {
-    if (e < d) out[e] = 0;
+    if (e0 < d) *reinterpret_cast<uint32_t*>(out + e0) = 0u;
     return;
   }
   const int pos = sv.slot_pos[m];
   const int nc = pos / ATTN_CHUNK + 1;
   const float* pml = w.part_ml + ((size_t)m * nq + h) * w.nchunk * 2;
-  float mx = -INFINITY;
-  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, pml[c * 2]);
-  float l = 0.f, acc = 0.f;
   const float* po = w.part_o + ((size_t)m * nq + h) * w.nchunk * d;
-  for (int c = 0; c < nc; ++c) {
-    const float cm = pml[c * 2];
-    const float f = (cm == -INFINITY) ? 0.f : __expf(cm - mx);
-    l += pml[c * 2 + 1] * f;
-    if (e < d) acc += po[(size_t)c * d + e] * f;
+  float mx = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
+  constexpr int UN = 8;
+  for (int c0 = 0; c0 < nc; c0 += UN) {
+    float2 ml[UN], ov[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int c = c0 + u;
+      ml[u] = make_float2(-INFINITY, 0.f);
+      ov[u] = make_float2(0.f, 0.f);
+      if (c < nc) {
+        ml[u] = *reinterpret_cast<const float2*>(pml + (size_t)c * 2);
+        if (e0 < d) ov[u] = *reinterpret_cast<const float2*>(po + (size_t)c * d + e0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const float cm = ml[u].x;
+      if (cm == -INFINITY) continue;  // a chunk with no visible key
+      const float nm = fmaxf(mx, cm);
+      const float fo = (mx == -INFINITY) ? 0.f : __expf(mx - nm);
+      const float fn = __expf(cm - nm);
+      l = l * fo + ml[u].y * fn;
+      a0 = a0 * fo + ov[u].x * fn;
+      a1 = a1 * fo + ov[u].y * fn;
+      mx = nm;
+    }
   }
-  if (e < d) out[e] = f32_to_bf16(acc / l);
+  if (e0 < d) {
+    const float inv = 1.0f / l;
+    *reinterpret_cast<uint32_t*>(out + e0) = (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
+  }
 }
 
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
@@ -350,7 +375,7 @@ int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, i
   const float scale = 1.0f / sqrtf((float)d);
   hipLaunchKernelGGL(attn_partial_kernel, dim3(R * nkv, w.nchunk), dim3(256), 0, st, q, kv, sv, nq, nkv, d, scale, w);
   MC_HIP(hipGetLastError());
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(M, nq), dim3(128), 0, st, sv, nq, d, w, att);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((M * nq + 3) / 4), dim3(256), 0, st, sv, M, nq, d, w, att);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }

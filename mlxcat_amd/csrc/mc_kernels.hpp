@@ -24,7 +24,7 @@ struct KVLayer {
   int cap;
 };
 
-// x[m][:] = embedding row of slot_tok[m]; ssq[t * ss_ld + m] = sum of squares of x[m][16t : 16t + 16]
+// x[m][:] = embedding row of slot_tok[m]; ssq[m * ss_ld + t] = sum of squares of x[m][16t : 16t + 16]
 int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16_t* x, float* ssq, int ss_ld,
                  hipStream_t st);
 // qkv [M][(nq + 2 nkv) d] -> q [M][nq d] (normed + rotated), K/V cache append for valid slots

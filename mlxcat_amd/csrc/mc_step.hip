@@ -159,6 +159,22 @@ __device__ inline uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
   return t;
 }
 
+__device__ inline unsigned long long block_max_u64(unsigned long long v, uint64_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long w = (unsigned long long)__shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  unsigned long long t = 0ull;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = red[w] > t ? red[w] : t;
+  __syncthreads();
+  return t;
+}
+
 __device__ inline float block_max_f(float v, float* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -333,7 +349,17 @@ __global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, 
   const uint16_t* lg = logits + (size_t)slot * s.V;
   const int V = s.V;
   if (s.temp[r] == 0.0f) {
-    const int t = block_argmax(lg, V, redf, redi);
+    int t;
+    if (s.amax) {
+      // max over the head's per-tile partials (value key << 32 | 0xFFFFFFFF - index)
+      const unsigned long long* ap = s.amax + (size_t)slot * s.amax_nt;
+      unsigned long long best = 0ull;
+      for (int i = threadIdx.x; i < s.amax_nt; i += blockDim.x) best = ap[i] > best ? ap[i] : best;
+      best = block_max_u64(best, red);
+      t = (int)(0xFFFFFFFFull - (best & 0xFFFFFFFFull));
+    } else {
+      t = block_argmax(lg, V, redf, redi);
+    }
     if (threadIdx.x == 0) s.scan_tok[r * s.K1 + j] = t;
     return;
   }

@@ -47,6 +47,9 @@ struct StepState {
   int32_t* out_cnt = nullptr;   // [R]
   int32_t* out_fin = nullptr;   // [R]
   unsigned long long* stats = nullptr;  // proposed, accepted, proposal_batches, rejected_batches
+  // greedy argmax partials of the verify logits written by the head (NULL: scan the logits)
+  const unsigned long long* amax = nullptr;  // [slot][amax_nt]
+  int amax_nt = 0;
 };
 
 int launch_propose(const StepState& s, hipStream_t st);
