@@ -9,8 +9,9 @@ positions copied from earlier spans.  A step is one speculative step (n-gram pro
 the timed region.  The same workload at batch 8 is reported beside it.
 
 Prints one JSON line: accepted tokens/s at batch 1 (value), the batch-8 figure, the
-verify-step latency, the live HBM roofline of the dominant kernel (the dequant GEMV,
-timed with HIP events on its stream) and the CPU oracle timed on a bounded sample.
+verify-step latency, the live HBM roofline of the dominant kernel (the persistent forward
+kernel when the step runs it, else the dequant GEMV; timed with HIP events on its stream)
+and the CPU oracle timed on a bounded sample.
 """
 from __future__ import annotations
 
@@ -48,7 +49,7 @@ def step_bytes(cfg: dict, ctx_lens, M: int) -> float:
     return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
 
 
-def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
+def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forward_mode: int = 1):
     from mlxcat_amd import _lib as hip
     from mlxcat_amd.workloads import copy_span_prompt
     L = hip.load()
@@ -59,6 +60,7 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
     max_new = (warmup + steps + 8) * (K_DRAFT + 1) + 8
     ctx = PROMPT_LEN + max_new + K_DRAFT + 16
     b = hip.Batch(m, rows, ctx, spec_cfg(rows))
+    b.set_fused(forward_mode)
     for r in range(rows):
         p = copy_span_prompt(SEED + r, PROMPT_LEN, QWEN3_4B["vocab"])
         b.insert(r, p, max_new, hip.make_sampling())
@@ -79,17 +81,20 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
                bytes_per_step=step_bytes(QWEN3_4B, kv0, rows * (K_DRAFT + 1)))
     out["step_hbm_gbs"] = out["bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
     if profile:
+        # kind 3: the persistent forward (one launch per step); kind 0: the dequant GEMVs
         b.set_profiling(True)
-        g_ms = g_by = 0.0
-        g_n = 0
+        acc = {k: [0.0, 0.0, 0] for k in (0, 3)}
         for _ in range(3):
             b.step()
-            ms, by, n = b.profile(0)
-            g_ms += ms
-            g_by += by
-            g_n += n
+            for k in (0, 3):
+                ms, by, n = b.profile(k)
+                acc[k][0] += ms
+                acc[k][1] += by
+                acc[k][2] += n
         b.set_profiling(False)
-        out["gemv"] = dict(ms=g_ms / 3, bytes=g_by / 3, launches=g_n // 3)
+        k = 3 if acc[3][2] > 0 else 0
+        out["dominant"] = dict(ms=acc[k][0] / 3, bytes=acc[k][1] / 3, launches=acc[k][2] // 3,
+                               kernel="fused_forward_kernel" if k == 3 else "qgemv_kernel<1>")
     b.close()
     m.close()
     return out
@@ -129,15 +134,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--forward", choices=["auto", "fused", "multi"], default="auto",
+                    help="verify forward: persistent kernel when possible (auto), required, or never")
     a = ap.parse_args()
+    mode = {"auto": 1, "fused": 2, "multi": 0}[a.forward]
     if a.gpus != 1:
         print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
-    b1 = run_gpu(1, a.steps, a.warmup, profile=True)
-    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False)
+    b1 = run_gpu(1, a.steps, a.warmup, profile=True, forward_mode=mode)
+    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False,
+                                      forward_mode=0 if mode == 0 else 1)
     cpu = None if a.no_cpu else run_cpu()
-    g = b1["gemv"]
+    g = b1["dominant"]
     achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
     line = {
         "metric": "accepted tok/s (bs=1,8) Qwen3-4B-shape 4-bit K=5; verify HBM GB/s %peak",
@@ -163,7 +172,7 @@ def main():
                             "bytes_per_step": b1["bytes_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qgemv_kernel<1>", "launches_per_step": g["launches"],
+                     "kernel": g["kernel"], "launches_per_step": g["launches"],
                      "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 3),
                      "alg_bytes_per_launch": round(g["bytes"] / max(1, g["launches"]))},
         "batch8": None if b8 is None else {"tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 4),

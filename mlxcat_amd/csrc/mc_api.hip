@@ -10,6 +10,7 @@
 #include <string>
 #include <vector>
 
+#include "mc_fused.hpp"
 #include "mc_gemv.hpp"
 #include "mc_kernels.hpp"
 #include "mc_step.hpp"
@@ -344,6 +345,8 @@ struct mc_batch {
            *logits = nullptr;
   float* gemv_part = nullptr;
   unsigned* gemv_cnt = nullptr;
+  size_t gemv_part_n = 0;  // floats
+  int gemv_cnt_n = 0;
   float* ssq = nullptr;  // [Mmax][hidden / 16]: per-tile sums of squares of the residual stream
   unsigned long long* amax = nullptr;  // [Mmax][vocab tiles]: greedy argmax partials of the head
   AttnWork aw{};
@@ -352,7 +355,7 @@ struct mc_batch {
   // pinned staging
   int32_t* h_i32 = nullptr;  // general staging
   size_t h_i32_n = 0;
-  int32_t* h_out = nullptr;  // [R*K1 tok | R cnt | R fin | R nprop | R kv_len]
+  int32_t* h_out = nullptr;  // [R*K1 tok | R cnt | R fin | R nprop | R kv_len | persistent-forward error]
   hipGraphExec_t graph = nullptr;
   hipGraph_t graph_def = nullptr;
   std::vector<int32_t> widths;
@@ -364,8 +367,16 @@ struct mc_batch {
   size_t ev_used = 0;
   struct Rec { int kind; size_t e0, e1; double bytes; };
   std::vector<Rec> recs;
-  double prof_ms[3] = {0, 0, 0}, prof_bytes[3] = {0, 0, 0};
-  int prof_launch[3] = {0, 0, 0};
+  double prof_ms[4] = {0, 0, 0, 0}, prof_bytes[4] = {0, 0, 0, 0};
+  int prof_launch[4] = {0, 0, 0, 0};
+  // persistent forward (mc_fused): at most FW_MMAX tokens over at most FW_MMAX rows
+  int fused_mode = 1;            // 0 off, 1 whenever the call allows it, 2 required
+  bool fused_ok = false;         // model and batch shape supported
+  FwArgs fw{};                   // fixed arguments; M and the logits flag are set per call
+  FwLayer* fw_layers = nullptr;  // device [n_layers]
+  unsigned long long* fw_ll = nullptr;
+  unsigned* fw_ctl = nullptr;    // [0] forward-call counter (starts at 1), [1] error word
+  int fw_grid = 0;
 };
 
 static void batch_free(mc_batch* b) {
@@ -375,7 +386,8 @@ static void batch_free(mc_batch* b) {
   if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
-                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch})
+                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
+                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -392,6 +404,81 @@ static int stage_i32(mc_batch* b, size_t n) {
   b->h_i32 = nullptr;
   MC_HIP(hipHostMalloc((void**)&b->h_i32, n * 4, hipHostMallocDefault));
   b->h_i32_n = n;
+  return MC_OK;
+}
+
+// Persistent-forward resources, when the model and the batch allow them (at most FW_MMAX
+// rows).  Not an error otherwise: the multi-kernel forward serves every call.
+static int fused_setup(mc_batch* b, int kcap) {
+  mc_model* m = b->m;
+  const auto& c = m->cfg;
+  const char* why = nullptr;
+  if (b->R > FW_MMAX || !fused_supported(c, 1, kcap, &why)) return MC_OK;
+  const int grid = fused_grid(m->device);
+  if (grid < 1) return MC_OK;
+  std::vector<FwLayer> hl((size_t)c.n_layers);
+  int oks = 1, dks = 1;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const auto& L = m->layers[(size_t)l];
+    FwLayer& f = hl[(size_t)l];
+    f.qkv = fused_lin(L.qkv, 1);
+    f.o = fused_lin(L.o, 4);
+    f.gu = fused_lin(L.gateup, 1);
+    f.dn = fused_lin(L.down, 4);
+    if (!f.qkv.ks || !f.o.ks || !f.gu.ks || !f.dn.ks) return MC_OK;
+    oks = std::max(oks, f.o.ks);
+    dks = std::max(dks, f.dn.ks);
+    f.in_norm = L.in_norm;
+    f.post_norm = L.post_norm;
+    f.q_norm = L.q_norm;
+    f.k_norm = L.k_norm;
+    f.k = b->kv[(size_t)l].k;
+    f.v = b->kv[(size_t)l].v;
+  }
+  const FwLin head = fused_lin(m->head(), 1);
+  if (!head.ks) return MC_OK;
+  int rc;
+  if ((rc = dev_alloc(&b->fw_layers, hl.size()))) return rc;
+  MC_HIP(hipMemcpy(b->fw_layers, hl.data(), hl.size() * sizeof(FwLayer), hipMemcpyHostToDevice));
+  const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
+  const size_t Nqkv = (size_t)(nq + 2 * nkv) * d;
+  const int npb = fused_npb_cap(kcap);
+  const size_t mm = FW_MMAX;
+  const size_t n_x = mm * H / 2, n_xss = mm * H / 16, n_qkv = mm * Nqkv / 2, n_att = mm * nq * d / 2,
+               n_act = mm * I / 2, n_op = (size_t)oks * mm * H, n_dp = (size_t)dks * mm * H,
+               n_ao = (size_t)b->R * nkv * npb * FW_QROWS * d, n_aml = (size_t)b->R * nkv * npb * FW_QROWS * 2;
+  if ((rc = dev_zero(&b->fw_ll, n_x + n_xss + n_qkv + n_att + n_act + n_op + n_dp + n_ao + n_aml))) return rc;
+  if ((rc = dev_zero(&b->fw_ctl, 2))) return rc;
+  const unsigned one = 1u;
+  MC_HIP(hipMemcpy(b->fw_ctl, &one, 4, hipMemcpyHostToDevice));
+  FwArgs& a = b->fw;
+  unsigned long long* p = b->fw_ll;
+  a.x = p; p += n_x;
+  a.xss = p; p += n_xss;
+  a.qkv = p; p += n_qkv;
+  a.att = p; p += n_att;
+  a.act = p; p += n_act;
+  a.opart = p; p += n_op;
+  a.dpart = p; p += n_dp;
+  a.ao = p; p += n_ao;
+  a.aml = p;
+  a.npb_cap = npb;
+  a.layers = b->fw_layers;
+  a.L = c.n_layers;
+  a.embed = m->embed;
+  a.head = head;
+  a.final_norm = m->final_norm;
+  a.H = H; a.nq = nq; a.nkv = nkv; a.d = d; a.I = I; a.V = c.vocab;
+  a.eps = c.rms_eps;
+  a.scale = 1.0f / sqrtf((float)d);
+  a.rope_cos = b->rope_cos;
+  a.rope_sin = b->rope_sin;
+  a.cap = kcap;
+  a.R = b->R;
+  a.epoch = b->fw_ctl;
+  a.err = b->fw_ctl + 1;
+  b->fw_grid = grid;
+  b->fused_ok = true;
   return MC_OK;
 }
 
@@ -423,13 +510,14 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   const int M = b->Mmax;
   if (!m->fake) {
     const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
-    const size_t per = (size_t)b->R * nkv * (size_t)max_ctx * d;
+    const int kcap = (max_ctx + 63) / 64 * 64;  // position stride of the cache
+    const size_t per = (size_t)b->R * nkv * (size_t)kcap * d;
     if ((rc = dev_zero(&b->kv_mem, per * 2 * (size_t)c.n_layers))) { batch_free(b); return rc; }
     b->kv.resize((size_t)c.n_layers);
     for (int l = 0; l < c.n_layers; ++l) {
       b->kv[(size_t)l].k = b->kv_mem + per * 2 * (size_t)l;
       b->kv[(size_t)l].v = b->kv_mem + per * (2 * (size_t)l + 1);
-      b->kv[(size_t)l].cap = max_ctx;
+      b->kv[(size_t)l].cap = kcap;
     }
     // RoPE table in double precision, rounded to float (shared definition with the oracle)
     const int hd = d / 2;
@@ -451,19 +539,22 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
       batch_free(b);
       return rc;
     }
-    // split-K workspace: the largest plan over every linear and m-tile class
+    // split-K workspace: the largest plan over every linear and m-tile class.  Units with
+    // a residual epilogue leave a partial here even with one K-range, so every plan counts.
     size_t part = 1;
     int maxnt = 1;
     auto acc_plan = [&](const QLinear& L) {
       for (int MT = 1; MT <= 4; ++MT) {
         int kr, ks;
         gemv_plan(L, MT, &kr, &ks);
-        if (ks > 1) part = std::max(part, (size_t)ks * L.NT * MT * 64 * 4);
+        part = std::max(part, (size_t)ks * L.NT * MT * 64 * 4);
       }
       maxnt = std::max(maxnt, L.NT);
     };
     for (auto& L : m->layers) { acc_plan(L.qkv); acc_plan(L.o); acc_plan(L.gateup); acc_plan(L.down); }
     acc_plan(m->head());
+    b->gemv_part_n = part;
+    b->gemv_cnt_n = maxnt;
     if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt)) ||
         (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M)) ||
         (rc = dev_zero(&b->amax, (size_t)M * m->head().NT))) {
@@ -476,6 +567,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
       batch_free(b);
       return rc;
     }
+    if ((rc = fused_setup(b, kcap))) { batch_free(b); return rc; }
   }
   if ((rc = dev_zero(&b->logits, (size_t)M * V))) { batch_free(b); return rc; }
 
@@ -516,7 +608,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     MC_HIP(hipMemcpy(s.reject, neg.data(), R * 4, hipMemcpyHostToDevice));
   }
   if ((rc = stage_i32(b, std::max<size_t>(4096, (size_t)b->hcap + 16)))) { batch_free(b); return rc; }
-  MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R) * 4, hipHostMallocDefault));
+  MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R + 1) * 4, hipHostMallocDefault));
   *out = b;
   return MC_OK;
 }
@@ -540,6 +632,51 @@ static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
   const size_t e1 = b->ev_used++;
   MC_HIP(hipEventRecord(b->ev[e1], b->st));
   b->recs.push_back({kind, e0, e1, bytes});
+  return MC_OK;
+}
+
+// The persistent forward over the M slots described in the StepState arrays (all rows of
+// the batch, at most FW_MMAX), logits for every slot when with_logits.
+static int fused_forward(mc_batch* b, int M, bool with_logits) {
+  FwArgs a = b->fw;
+  const StepState& s = b->s;
+  a.M = M;
+  a.with_head = with_logits ? 1 : 0;
+  a.slot_tok = s.slot_tok;
+  a.slot_row = s.slot_row;
+  a.row_slot0 = s.row_slot0;
+  a.n_valid = s.n_valid;
+  a.qbase = s.qbase;
+  a.logits = b->logits;
+  a.amax = b->amax;
+  int rc = launch_fused_forward(a, b->fw_grid, b->st);
+  if (rc) return rc;
+  return launch_epoch_bump(b->fw_ctl, b->st);
+}
+
+// Algorithmic HBM bytes of one forward over M slots: every linear's packed weights
+// (0.5625 B per weight), the cached K/V read, the new K/V written, the bf16 logits.
+static double forward_alg_bytes(const mc_batch* b, int M, bool with_head) {
+  const mc_model* m = b->m;
+  const auto& c = m->cfg;
+  double w = 0;
+  for (const auto& L : m->layers) w += L.qkv.alg_bytes() + L.o.alg_bytes() + L.gateup.alg_bytes() + L.down.alg_bytes();
+  if (with_head) w += m->head().alg_bytes() + (double)M * c.vocab * 2;
+  double ctx = 0;
+  for (int r = 0; r < b->R; ++r) ctx += b->kv_len_host[(size_t)r];
+  const double kv_row = (double)c.n_layers * 2 * c.n_kv_heads * c.head_dim * 2;
+  return w + ctx * kv_row + (double)M * kv_row;
+}
+
+// Whether this forward runs as the persistent kernel.
+static bool use_fused(const mc_batch* b, int M) { return b->fused_ok && b->fused_mode != 0 && M >= 1 && M <= FW_MMAX; }
+
+// The persistent forward's error word (nonzero: a wait timed out or the unit schedule broke).
+static int fused_check(mc_batch* b) {
+  if (!b->fused_ok) return MC_OK;
+  unsigned e = 0;
+  MC_HIP(hipMemcpy(&e, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost));
+  if (e) return fail(MC_E_STATE, e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
   return MC_OK;
 }
 
@@ -567,7 +704,8 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
     a.y = y + (size_t)m0 * ldy; a.ldy = ldy;
     a.M = mc; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
     gemv_plan(L, MT, &a.kr, &a.ksplit);
-    a.part = b->gemv_part; a.counters = b->gemv_cnt; a.epi = epi;
+    a.part = b->gemv_part; a.part_floats = b->gemv_part_n;
+    a.counters = b->gemv_cnt; a.counters_n = b->gemv_cnt_n; a.epi = epi;
     if (amax) a.amax = amax + (size_t)m0 * L.NT;
     size_t e0 = 0;
     int rc = prof_begin(b, &e0);
@@ -589,6 +727,14 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
     if (lgn > 0) return launch_fake_logits(c.arch, s.slot_tok + lg0, lgn, c.vocab, b->logits + (size_t)lg0 * c.vocab, b->st);
     return MC_OK;
   }
+  if (use_fused(b, M)) {
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    if ((rc = fused_forward(b, M, lgn > 0))) return rc;
+    if ((rc = prof_end(b, e0, 3, forward_alg_bytes(b, M, lgn > 0)))) return rc;
+    return MC_OK;
+  }
+  if (b->fused_mode == 2) return fail(MC_E_STATE, "persistent forward required but not available for this call");
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
@@ -694,7 +840,7 @@ extern "C" int mc_forward(mc_batch* b, int32_t nrows, const int32_t* rows, const
     MC_HIP(hipMemcpyAsync(logits_host, b->logits, (size_t)M * b->m->cfg.vocab * 2, hipMemcpyDeviceToHost, b->st));
   }
   MC_HIP(hipStreamSynchronize(b->st));
-  return MC_OK;
+  return fused_check(b);
 }
 
 // --------------------------- admission ------------------------------------
@@ -875,11 +1021,24 @@ extern "C" int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t
   MC_HIP(hipSetDevice(b->m->device));
   if ((rc = sync_kv_len(b))) return rc;
   const int len = b->kv_len_host[(size_t)row];
-  const uint16_t* src = which_v ? b->kv[(size_t)layer].v : b->kv[(size_t)layer].k;
-  for (int h = 0; h < c.n_kv_heads; ++h)
-    MC_HIP(hipMemcpy(out + (size_t)h * len * c.head_dim,
-                     src + (((size_t)row * c.n_kv_heads + h) * b->cap) * c.head_dim, (size_t)len * c.head_dim * 2,
-                     hipMemcpyDeviceToHost));
+  const KVLayer& kv = b->kv[(size_t)layer];
+  const int d = c.head_dim;
+  if (!which_v) {
+    for (int h = 0; h < c.n_kv_heads; ++h)
+      MC_HIP(hipMemcpy(out + (size_t)h * len * d, kv.k + (((size_t)row * c.n_kv_heads + h) * kv.cap) * d,
+                       (size_t)len * d * 2, hipMemcpyDeviceToHost));
+    return MC_OK;
+  }
+  // V is stored transposed ([d][cap] per head): copy the d rows, then transpose
+  std::vector<uint16_t> tmp((size_t)d * len);
+  for (int h = 0; h < c.n_kv_heads; ++h) {
+    if (len > 0)
+      MC_HIP(hipMemcpy2D(tmp.data(), (size_t)len * 2, kv.v + ((size_t)row * c.n_kv_heads + h) * d * kv.cap,
+                         (size_t)kv.cap * 2, (size_t)len * 2, (size_t)d, hipMemcpyDeviceToHost));
+    uint16_t* o = out + (size_t)h * len * d;
+    for (int e = 0; e < d; ++e)
+      for (int p = 0; p < len; ++p) o[(size_t)p * d + e] = tmp[(size_t)e * len + p];
+  }
   return MC_OK;
 }
 
@@ -959,7 +1118,13 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
   MC_HIP(hipMemcpyAsync(h + R * K1 + R, s.out_fin, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipMemcpyAsync(h + R * K1 + 2 * R, s.nprop, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipMemcpyAsync(h + R * K1 + 3 * R, s.kv_len, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  h[R * K1 + 4 * R] = 0;
+  if (b->fused_ok) MC_HIP(hipMemcpyAsync(h + R * K1 + 4 * R, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipStreamSynchronize(b->st));
+  if (h[R * K1 + 4 * R]) {
+    const unsigned e = (unsigned)h[R * K1 + 4 * R];
+    return fail(MC_E_STATE, e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
+  }
   if (out_tokens) memcpy(out_tokens, h, (size_t)R * K1 * 4);
   if (out_counts) memcpy(out_counts, h + R * K1, (size_t)R * 4);
   if (out_finish) memcpy(out_finish, h + R * K1 + R, (size_t)R * 4);
@@ -968,7 +1133,7 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
     b->kv_len_host[(size_t)r] = h[R * K1 + 3 * R + r];
   }
   if (b->profiling) {
-    for (int k = 0; k < 3; ++k) { b->prof_ms[k] = 0; b->prof_bytes[k] = 0; b->prof_launch[k] = 0; }
+    for (int k = 0; k < 4; ++k) { b->prof_ms[k] = 0; b->prof_bytes[k] = 0; b->prof_launch[k] = 0; }
     for (const auto& rec : b->recs) {
       float ms = 0;
       MC_HIP(hipEventElapsedTime(&ms, b->ev[rec.e0], b->ev[rec.e1]));
@@ -1000,6 +1165,21 @@ extern "C" int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap) {
   return n;
 }
 
+extern "C" int mc_batch_set_fused(mc_batch* b, int32_t mode) {
+  if (!b || mode < 0 || mode > 2) return fail(MC_E_INVALID, "mc_batch_set_fused: bad argument");
+  if (mode == 2 && !b->fused_ok) return fail(MC_E_STATE, "persistent forward not available for this model / batch");
+  b->fused_mode = mode;
+  if (b->graph) {  // the captured step follows the mode it was captured with
+    MC_HIP(hipGraphExecDestroy(b->graph));
+    b->graph = nullptr;
+    if (b->graph_def) MC_HIP(hipGraphDestroy(b->graph_def));
+    b->graph_def = nullptr;
+  }
+  return MC_OK;
+}
+
+extern "C" int mc_batch_fused_available(mc_batch* b) { return b && b->fused_ok ? 1 : 0; }
+
 extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
   if (!b) return fail(MC_E_INVALID, "null batch");
   b->profiling = enabled != 0;
@@ -1007,7 +1187,7 @@ extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
 }
 
 extern "C" int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches) {
-  if (!b || kind < 0 || kind > 2) return fail(MC_E_INVALID, "bad argument");
+  if (!b || kind < 0 || kind > 3) return fail(MC_E_INVALID, "bad argument");
   if (ms) *ms = b->prof_ms[kind];
   if (bytes) *bytes = b->prof_bytes[kind];
   if (launches) *launches = b->prof_launch[kind];

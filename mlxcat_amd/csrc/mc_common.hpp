@@ -8,6 +8,17 @@
 
 #include "../../include/mlxcat_hip.h"
 
+// Dynamic LDS and register-placement hints.  The CPU emulation of the kernels (tests/emu)
+// compiles the sources as host C++ and supplies its own definitions of these.
+#ifndef MC_EMULATE
+#define MC_DYN_LDS(name) extern __shared__ __align__(16) unsigned char name[]
+#define MC_OPAQUE(x) asm volatile("" : "+v"(x))
+#define MC_OPAQUE2(x, y) asm volatile("" : "+v"(x), "+v"(y))
+#define MC_FENCE() asm volatile("" ::: "memory")
+#define MC_TO_VGPR(dst, src) asm volatile("v_mov_b32 %0, %1" : "=v"(dst) : "s"(src))
+#define MC_TRACE_TIMEOUT(site) ((void)0)
+#endif
+
 namespace mc {
 
 // ---------------------------------------------------------------------------
@@ -120,10 +131,15 @@ __device__ inline uint64_t mass_of(float e) {
 // (w >> 4p) & 0x000F000F | 0x43004300 yields the bf16 pair (128 + q_2p, 128 + q_2p+1).
 //
 // Scales/biases: uint32 (scale bf16 | bias bf16 << 16) at
-// sb[((t * GP + gp) * 16 + r) * 2 + gi] for row 16t + r, group 2gp + gi: the lane that
-// owns weight row r of the tile reads its two groups with one 8-byte load.
+// sb[((t * 16 + r) * GP + gp) * 2 + gi] for row 16t + r, group 2gp + gi ([NT][16][GP][2]):
+// the lane that owns weight row r of the tile reads one group pair's two groups with one
+// 8-byte load, or two consecutive group pairs with one 16-byte load.
 // Rows >= N and groups >= K/64 are zero (scale = bias = 0, so they add nothing).
 // ---------------------------------------------------------------------------
+__host__ __device__ inline size_t tile_sb_word(int t, int r, int gp, int gi, int GP) {
+  return (((size_t)t * 16 + r) * GP + gp) * 2 + gi;
+}
+
 struct QLinear {
   int N = 0, K = 0, NT = 0, GP = 0;
   uint32_t* qw = nullptr;  // NT * GP * 256 words

@@ -86,12 +86,12 @@ struct WBuf {
 template <int D>
 __device__ inline void load_unit(WBuf<D>& w, const GemvArgs& a, int t, int gp0, int ngp, int wave, int lane, int r16) {
   const u32x4* qbase = reinterpret_cast<const u32x4*>(a.qw) + ((size_t)t * a.GP + gp0) * 64 + lane;
-  const uint2* sbase = reinterpret_cast<const uint2*>(a.sb) + ((size_t)t * a.GP + gp0) * 16 + r16;
+  const uint2* sbase = reinterpret_cast<const uint2*>(a.sb) + tile_sb_word(t, r16, gp0, 0, a.GP) / 2;
 #pragma unroll
   for (int i = 0; i < D; ++i) {
     const int j = min(wave + GEMV_WAVES * i, ngp - 1);  // a short K-range re-reads its last pair
     w.nib[i] = __builtin_nontemporal_load(qbase + (size_t)j * 64);
-    w.sb[i] = sbase[(size_t)j * 16];
+    w.sb[i] = sbase[j];
   }
 }
 
@@ -240,7 +240,7 @@ __device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16
 // compiler's load counters keep the prefetch outstanding during the compute.
 template <int MT, int D, int U>
 __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
+  MC_DYN_LDS(smem);
   const int kr_gp = a.kr;
   const int XS = xrow_stride(kr_gp);
   const int Mr = min(a.M, 16 * MT);
@@ -394,7 +394,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   // one dequant constant in an SGPR, the other in a VGPR: v_and_or_b32 may read one SGPR
   const uint32_t mask = a.dq_mask;
   uint32_t magic;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(magic) : "s"(a.dq_magic));
+  MC_TO_VGPR(magic, a.dq_magic);
   const bool deferred = ks > 1 || a.epi == EPI_RESIDUAL;
   f32x4 acc[MT];
   const int u0 = u;
@@ -520,6 +520,9 @@ int gemv_launch(const GemvArgs& a, int MT, hipStream_t st) {
   if (a.amax && a.epi != EPI_STORE) return fail(MC_E_INVALID, "gemv: argmax partials need the store epilogue");
   if (a.epi == EPI_RESIDUAL && (a.N % 16 || (a.ss_out && a.ss_ld_out < a.NT)))
     return fail(MC_E_INVALID, "gemv: residual epilogue needs N % 16 == 0");
+  if ((a.ksplit > 1 || a.epi == EPI_RESIDUAL) &&
+      (!a.part || a.part_floats < (size_t)a.ksplit * a.NT * MT * 64 * 4 || !a.counters || a.counters_n < a.NT))
+    return fail(MC_E_INVALID, "gemv: split-K workspace smaller than the plan");
   const int D = (a.kr + GEMV_WAVES - 1) / GEMV_WAVES;  // group pairs per wave per unit
   switch (MT) {
     case 1: launch_mt<1>(a, D, lds, st); break;
@@ -573,7 +576,7 @@ __device__ inline size_t tile_word_index(const QLinear& L, int nd, int kw) {
 __device__ inline size_t tile_sb_index(const QLinear& L, int nd, int g) {
   const int t = nd >> 4, r = nd & 15;
   const int gp = g >> 1, gi = g & 1;
-  return (((size_t)t * L.GP + gp) * 16 + r) * 2 + gi;
+  return tile_sb_word(t, r, gp, gi, L.GP);
 }
 
 __global__ void repack_kernel(QLinear L, int row_off, int row_stride, int Nsrc, const uint32_t* wq,

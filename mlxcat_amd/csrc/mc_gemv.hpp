@@ -26,7 +26,9 @@ struct GemvArgs {
   int M = 0, N = 0, K = 0, NT = 0, GP = 0;
   int kr = 0, ksplit = 1;            // group pairs per K-range, K-ranges
   float* part = nullptr;             // split-K partials [ksplit][NT][MT][64][4]
+  size_t part_floats = 0;            // capacity of part (checked at launch)
   unsigned* counters = nullptr;      // [NT], zero at rest
+  int counters_n = 0;                // capacity of counters (checked at launch)
   int epi = EPI_STORE;
   uint32_t dq_mask = 0x000F000Fu, dq_magic = 0x43004300u;  // nibble-pair -> bf16 (128 + q) constants
   // EPI_STORE only, non-null: amax[m * NT + t] = max over the tile's 16 rows of

@@ -34,7 +34,7 @@ __global__ void embed_kernel(QLinear E, const int32_t* slot_tok, int M, int H, u
     const int g = kw >> 3, w8 = kw & 7, am = w8 >> 2, c = w8 & 3;
     const int gp = g >> 1, gi = g & 1;
     const uint32_t word = E.qw[(((size_t)t * E.GP + gp) * 64 + c * 16 + r) * 4 + gi * 2 + am];
-    const uint32_t sbw = E.sb[(((size_t)t * E.GP + gp) * 16 + r) * 2 + gi];
+    const uint32_t sbw = E.sb[tile_sb_word(t, r, gp, gi, E.GP)];
     const float s = bf16_to_f32((uint16_t)(sbw & 0xFFFFu)), b = bf16_to_f32((uint16_t)(sbw >> 16));
     uint32_t out[4];
 #pragma unroll
@@ -98,8 +98,8 @@ __global__ void __launch_bounds__(256) qk_rope_append_kernel(const uint16_t* qkv
     const uint16_t* hp = src + (size_t)hh * d;
     if (hh >= nq + nkv) {  // V head: copy into the cache
       const int h = hh - nq - nkv;
-      uint16_t* dst = kv.v + (((size_t)row * nkv + h) * kv.cap + pos) * d;
-      for (int i = lane; i < d; i += 64) dst[i] = hp[i];
+      uint16_t* dst = kv.v + ((size_t)row * nkv + h) * d * kv.cap + pos;
+      for (int i = lane; i < d; i += 64) dst[(size_t)i * kv.cap] = hp[i];
       return;
     }
     const bool is_q = hh < nq;
@@ -187,23 +187,29 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const uint16_t* q, KV
   const int slot0 = sv.row_slot0[r];
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
 
-  // ---- stage the chunk: 16-byte loads, K row-major, V transposed; keys >= nk are zero ----
+  // ---- stage the chunk: 16-byte loads of K [key][d] and of V^T [d][key] (the cache
+  // layout); keys >= nk are zero ----
   const uint16_t* kbase = kv.k + (((size_t)r * nkv + kh) * kv.cap + k0) * d;
-  const uint16_t* vbase = kv.v + (((size_t)r * nkv + kh) * kv.cap + k0) * d;
+  const uint16_t* vbase = kv.v + ((size_t)r * nkv + kh) * d * kv.cap + k0;
   const int cpk = d / 8;  // 16-byte chunks per key row
   for (int i = tid; i < ATTN_CHUNK * cpk; i += 256) {
     const int key = i / cpk, e = (i - key * cpk) * 8;
-    u4 kk = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-    if (key < nk) {
-      kk = *reinterpret_cast<const u4*>(kbase + (size_t)key * d + e);
-      vv = *reinterpret_cast<const u4*>(vbase + (size_t)key * d + e);
-    }
+    u4 kk = {0u, 0u, 0u, 0u};
+    if (key < nk) kk = *reinterpret_cast<const u4*>(kbase + (size_t)key * d + e);
     *reinterpret_cast<u4*>(ks + key * KS_STRIDE + e) = kk;
+  }
+  for (int i = tid; i < d * (ATTN_CHUNK / 8); i += 256) {
+    const int e = i / (ATTN_CHUNK / 8), kc = (i % (ATTN_CHUNK / 8)) * 8;
+    u4 vv = {0u, 0u, 0u, 0u};
+    if (kc < nk) {
+      vv = *reinterpret_cast<const u4*>(vbase + (size_t)e * kv.cap + kc);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      vt[(e + 2 * h) * VT_STRIDE + key] = (uint16_t)(vv[h] & 0xFFFFu);
-      vt[(e + 2 * h + 1) * VT_STRIDE + key] = (uint16_t)(vv[h] >> 16);
+      for (int h = 0; h < 4; ++h) {  // zero the keys >= nk
+        if (kc + 2 * h >= nk) vv[h] &= 0xFFFF0000u;
+        if (kc + 2 * h + 1 >= nk) vv[h] &= 0x0000FFFFu;
+      }
     }
+    *reinterpret_cast<u4*>(vt + e * VT_STRIDE + kc) = vv;
   }
   // d < 128: zero the unused d rows of V^T and d columns of K so the MFMA steps see zeros
   for (int i = tid; i < (128 - d) * ATTN_CHUNK; i += 256) {
@@ -414,8 +420,9 @@ __global__ void kv_synth_kernel(KVLayer kv, int layer, int row, int nkv, int d, 
                         ((uint64_t)p << 8));
     const uint64_t hh = mix64(seed ^ mix64(a) ^ (uint64_t)e);
     const uint32_t sign = (uint32_t)(hh & 1u), ex = 126u - (uint32_t)((hh >> 1) & 3u), mant = (uint32_t)((hh >> 3) & 0x7Fu);
-    uint16_t* c = wv ? kv.v : kv.k;
-    c[(((size_t)row * nkv + h) * kv.cap + p) * d + e] = (uint16_t)((sign << 15) | (ex << 7) | mant);
+    const uint16_t val = (uint16_t)((sign << 15) | (ex << 7) | mant);
+    if (wv) kv.v[(((size_t)row * nkv + h) * d + e) * kv.cap + p] = val;
+    else kv.k[(((size_t)row * nkv + h) * kv.cap + p) * d + e] = val;
   }
 }
 

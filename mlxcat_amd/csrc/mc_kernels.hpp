@@ -20,8 +20,9 @@ struct SlotView {
 
 struct KVLayer {
   uint16_t* k;  // [R][n_kv][cap][d]
-  uint16_t* v;  // [R][n_kv][cap][d]
-  int cap;
+  uint16_t* v;  // transposed: [R][n_kv][d][cap], so 8 consecutive positions of one
+                // dimension are one 16-byte load (the k operand of the P V product)
+  int cap;      // position stride, a multiple of 64
 };
 
 // x[m][:] = embedding row of slot_tok[m]; ssq[m * ss_ld + t] = sum of squares of x[m][16t : 16t + 16]
