@@ -128,7 +128,11 @@ __device__ inline uint64_t mass_of(float e) {
 // [2gp+1, MFMA 0], [2gp+1, MFMA 1].  MFMA a of group g covers physical k =
 // 64g + 32a + 8c + i, i = 0..7, i.e. exactly MLX word kw = 8g + 4a + c.  Within a
 // word, element i sits at bits 4(i/2) for even i and 16 + 4(i/2) for odd i, so
-// (w >> 4p) & 0x000F000F | 0x43004300 yields the bf16 pair (128 + q_2p, 128 + q_2p+1).
+// ((w << 3) >> 4p) & 0x00780078 | 0x3F803F80 puts the nibble pair in the top four mantissa
+// bits of two bf16 ones: the pair (1 + q_2p / 16, 1 + q_2p+1 / 16).  A group's dot product
+// then folds as s q.x + b sum(x) = 16 s (v.x) - 16 s sum(x) + b sum(x): the offset (1) is
+// of the order of the signal (q / 16), so the fp32 accumulation of v.x loses no more than
+// a bit to the cancellation (an offset of 128 with q in the low bits would lose about 4).
 //
 // Scales/biases: uint32 (scale bf16 | bias bf16 << 16) at
 // sb[((t * 16 + r) * GP + gp) * 2 + gi] for row 16t + r, group 2gp + gi ([NT][16][GP][2]):
@@ -139,6 +143,9 @@ __device__ inline uint64_t mass_of(float e) {
 __host__ __device__ inline size_t tile_sb_word(int t, int r, int gp, int gi, int GP) {
   return (((size_t)t * 16 + r) * GP + gp) * 2 + gi;
 }
+constexpr uint32_t DQ_MASK = 0x00780078u;   // the nibble pair at mantissa bits 3..6
+constexpr uint32_t DQ_MAGIC = 0x3F803F80u;  // two bf16 ones
+constexpr float DQ_STEP = 16.0f;            // v = 1 + q / DQ_STEP
 
 struct QLinear {
   int N = 0, K = 0, NT = 0, GP = 0;

@@ -101,10 +101,10 @@ __device__ inline uint32_t pack2(float a, float b) { return (uint32_t)f32_to_bf1
 
 __device__ inline bf16x8 dequant_word(uint32_t w, uint32_t mask, uint32_t magic) {
   u32x4 p;
-  p.x = (w & mask) | magic;
-  p.y = ((w >> 4) & mask) | magic;
-  p.z = ((w >> 8) & mask) | magic;
-  p.w = ((w >> 12) & mask) | magic;
+  p.x = ((w << 3) & mask) | magic;
+  p.y = ((w >> 1) & mask) | magic;
+  p.z = ((w >> 5) & mask) | magic;
+  p.w = ((w >> 9) & mask) | magic;
   return __builtin_bit_cast(bf16x8, p);
 }
 __device__ inline float silu_f(float z) { return z / (1.0f + __expf(-z)); }
@@ -330,8 +330,8 @@ __device__ inline f32x4 gemv_compute(const u32x4 (&ub)[32], int ngp, const unsig
         const bf16x8 wv0 = dequant_word(gi ? wq.z : wq.x, mask, magic);
         const bf16x8 wv1 = dequant_word(gi ? wq.w : wq.y, mask, magic);
         const uint32_t sbv = (j & 1) ? (gi ? sbp.w : sbp.z) : (gi ? sbp.y : sbp.x);
-        const float sv = __uint_as_float(sbv << 16);
-        const float bv = __builtin_fmaf(-128.0f, sv, __uint_as_float(sbv & 0xFFFF0000u));
+        const float sv = DQ_STEP * __uint_as_float(sbv << 16);
+        const float bv = __uint_as_float(sbv & 0xFFFF0000u) - sv;
         const int kl = j * 128 + gi * 64;
         const bf16x8 xv0 = *reinterpret_cast<const bf16x8*>(xrow + kl);
         const bf16x8 xv1 = *reinterpret_cast<const bf16x8*>(xrow + kl + 32);
@@ -1093,9 +1093,9 @@ __global__ void __launch_bounds__(FW_THREADS) fused_forward_kernel(FwArgs a) {
   __syncthreads();
   const int na = fl[F_NA];
   // dequant constants: one in an SGPR, the other in a VGPR (v_and_or_b32 reads one SGPR)
-  const uint32_t mask = 0x000F000Fu;
+  const uint32_t mask = DQ_MASK;
   uint32_t magic;
-  MC_TO_VGPR(magic, 0x43004300u);
+  MC_TO_VGPR(magic, DQ_MAGIC);
 
   int nst = 0, nat = 0;
   WaveState ws;

@@ -31,14 +31,14 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-// mask = 0x000F000F, magic = 0x43004300, passed in registers so that each pair becomes
-// one v_and_or_b32 (VOP3 takes no literal operands on this architecture)
+// mask = DQ_MASK, magic = DQ_MAGIC, passed in registers so that each pair becomes a shift
+// and one v_and_or_b32 (VOP3 takes no literal operands on this architecture)
 __device__ inline bf16x8 dequant_word(uint32_t w, uint32_t mask, uint32_t magic) {
   u32x4 p;
-  p.x = (w & mask) | magic;
-  p.y = ((w >> 4) & mask) | magic;
-  p.z = ((w >> 8) & mask) | magic;
-  p.w = ((w >> 12) & mask) | magic;
+  p.x = ((w << 3) & mask) | magic;
+  p.y = ((w >> 1) & mask) | magic;
+  p.z = ((w >> 5) & mask) | magic;
+  p.w = ((w >> 9) & mask) | magic;
   return __builtin_bit_cast(bf16x8, p);
 }
 
@@ -113,8 +113,8 @@ __device__ inline void compute_unit(f32x4 (&acc)[MT], const WBuf<D>& w, const ui
       const bf16x8 wv0 = dequant_word(gi ? w.nib[i].z : w.nib[i].x, mask, magic);
       const bf16x8 wv1 = dequant_word(gi ? w.nib[i].w : w.nib[i].y, mask, magic);
       const uint32_t sbv = gi ? w.sb[i].y : w.sb[i].x;
-      const float sv = __uint_as_float(sbv << 16);
-      const float bv = __builtin_fmaf(-128.0f, sv, __uint_as_float(sbv & 0xFFFF0000u));
+      const float sv = DQ_STEP * __uint_as_float(sbv << 16);
+      const float bv = __uint_as_float(sbv & 0xFFFF0000u) - sv;
       const int kl = j * 128 + gi * 64;
       const int gl = j * 2 + gi;
 #pragma unroll

@@ -30,7 +30,7 @@ struct GemvArgs {
   unsigned* counters = nullptr;      // [NT], zero at rest
   int counters_n = 0;                // capacity of counters (checked at launch)
   int epi = EPI_STORE;
-  uint32_t dq_mask = 0x000F000Fu, dq_magic = 0x43004300u;  // nibble-pair -> bf16 (128 + q) constants
+  uint32_t dq_mask = DQ_MASK, dq_magic = DQ_MAGIC;  // nibble pair -> bf16 (1 + q / 16) constants
   // EPI_STORE only, non-null: amax[m * NT + t] = max over the tile's 16 rows of
   // (order-preserving key of the stored bf16 value) << 32 | (0xFFFFFFFF - row): the tile's
   // greedy argmax, lowest row on ties

@@ -154,6 +154,9 @@ int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t*
                      const int32_t* tokens, uint16_t* logits, uint16_t* hidden);
 
 void or_set_threads(int n);
+/* reversed != 0: every fp32 reduction of the forward (linears, RMSNorm, attention) runs in
+ * another order (test aid: the rounding noise floor between two exact summation orders) */
+void or_set_reduction_order(int reversed);
 
 /* y[M][N] = x[M][K] . dequant(W)^T for one MLX 4-bit affine g64 tensor (fp32 in/out);
  * the same per-output fixed-order reduction the forward uses. */

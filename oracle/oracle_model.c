@@ -43,6 +43,14 @@ struct or_model {
 };
 
 static int g_threads = 0;
+/* 1: every fp32 reduction runs in another order -- the linears sum their 64-wide groups
+ * last to first, RMSNorm and the attention dot products sum sequentially from the last
+ * element, softmax sums run over the keys last to first.  Mathematically the same forward;
+ * its distance from the default order is the rounding noise floor of a correct
+ * implementation that sums in another order. */
+static int g_reversed = 0;
+void or_set_reduction_order(int reversed) { g_reversed = reversed != 0; }
+
 void or_set_threads(int n) {
   g_threads = n;
 #ifdef _OPENMP
@@ -241,7 +249,8 @@ static void qlinear(const or_linear* L, const float* x, int M, float* y) {
 #pragma omp for schedule(static)
     for (int n = 0; n < N; ++n) {
       for (int m = 0; m < M; ++m) accm[m] = 0.0f;
-      for (int g = 0; g < G; ++g) {
+      for (int gi = 0; gi < G; ++gi) {
+        const int g = g_reversed ? G - 1 - gi : gi;
         for (int w = 0; w < 8; ++w) {
           uint32_t word = L->wq[(size_t)n * KW + g * 8 + w];
           for (int j = 0; j < 8; ++j) q[w * 8 + j] = (float)((word >> (4 * j)) & 0xFu);
@@ -279,6 +288,10 @@ static void rmsnorm(const float* x, const uint16_t* w, int n, float eps, float* 
     for (int j = 0; j < 8; ++j) a[j] += x[i + j] * x[i + j];
   for (; i < n; ++i) a[0] += x[i] * x[i];
   float ss = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+  if (g_reversed) {
+    ss = 0.0f;
+    for (int k = n - 1; k >= 0; --k) ss += x[k] * x[k];
+  }
   float r = 1.0f / sqrtf(ss / (float)n + eps);
   for (int k = 0; k < n; ++k) out[k] = bf(tobf((x[k] * r) * bf(w[k])));
 }
@@ -398,14 +411,20 @@ int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t*
           float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
           for (int i = 0; i < d; i += 8)
             for (int z = 0; z < 8; ++z) a[z] += qv[i + z] * bf(kk[i + z]);
-          float s = (((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))) * scale;
+          float dsum = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+          if (g_reversed) {
+            dsum = 0.0f;
+            for (int i = d - 1; i >= 0; --i) dsum += qv[i] * bf(kk[i]);
+          }
+          float s = dsum * scale;
           sc[j] = s;
           if (s > mx) mx = s;
         }
         float den = 0.0f;
         float acc[512];
         for (int i = 0; i < d; ++i) acc[i] = 0.0f;
-        for (int j = 0; j <= P; ++j) {
+        for (int jj = 0; jj <= P; ++jj) {
+          const int j = g_reversed ? P - jj : jj;
           float p = expf(sc[j] - mx);
           den += p;
           const uint16_t* vv = y->vc + kv_index(m, row, kh, j);

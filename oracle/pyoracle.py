@@ -98,6 +98,7 @@ def lib():
             "or_forward": (I, [P, I, P, P, P, P]),
             "or_forward_trace": (I, [P, I, P, P, P, P, P]),
             "or_set_threads": (None, [I]),
+            "or_set_reduction_order": (None, [I]),
             "or_generator_create": (P, [P, P, I, I, U64]),
             "or_generator_destroy": (None, [P]),
             "or_generator_insert": (I, [P, I, P, I, I, P, P]),
@@ -237,6 +238,18 @@ class Model:
         if rc:
             raise RuntimeError(f"or_forward failed: {rc}")
         return (lg, hid) if trace else lg
+
+
+class reversed_reduction_order:
+    """Context: every fp32 reduction of the oracle's forward runs in another order."""
+
+    def __enter__(self):
+        lib().or_set_reduction_order(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().or_set_reduction_order(0)
+        return False
 
 
 def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1) -> Sampling:

@@ -48,22 +48,64 @@ def assert_close_bf16(got_u16, want_u16, atol=ATOL, rtol=RTOL, what=""):
     w = bf16_to_f32(want_u16).astype(np.float64)
     err = np.abs(g - w)
     bad = err > atol + rtol * np.abs(w)
-    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outside {atol} abs + {rtol} rel; "
-                           f"max err {err.max():.4g}")
+    if bad.any():
+        i = np.unravel_index(int(np.argmax(np.where(bad, err, -1.0))), err.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside {atol} abs + {rtol} rel; "
+                             f"max err {err.max():.4g}; worst outlier at {tuple(int(x) for x in i)}: "
+                             f"got {g[i]:.6g} want {w[i]:.6g}")
 
 
-def assert_close_bf16_wide(got_u16, want_u16, atol=ATOL, rtol=RTOL, frac=0.999, what=""):
-    """Full-width decoders: bf16 rounding of the hidden state (2^-8 relative) flips in a
-    different place on each side and drifts through the layers, so a few logits land just
-    outside the elementwise bound.  Every logit must be within twice the bound, at least
-    `frac` of them within it, and greedy argmax must agree wherever the top-2 margin is clear."""
+def assert_close_bf16_kv(got_u16, want_u16, atol=ATOL, rtol=RTOL, frac=0.999, what=""):
+    """Cached K/V against the oracle.  K is RMS-normalised and then rotated (k0 cos - k1 sin):
+    a one-ulp bf16 rounding flip of a large component on either side lands on a small
+    rotated value as several of its ulps.  Every element must be within twice the logit
+    bound and at least `frac` of them within it."""
     g = bf16_to_f32(got_u16).astype(np.float64)
     w = bf16_to_f32(want_u16).astype(np.float64)
     err = np.abs(g - w)
     bound = atol + rtol * np.abs(w)
-    assert (err <= 2 * bound).all(), f"{what}: max err {err.max():.4g} beyond twice the bound"
+    if not (err <= 2 * bound).all():
+        i = np.unravel_index(int(np.argmax(err - 2 * bound)), err.shape)
+        raise AssertionError(f"{what}: element {tuple(int(x) for x in i)} got {g[i]:.6g} want {w[i]:.6g}, "
+                             f"beyond twice the bound")
     inside = float((err <= bound).mean())
     assert inside >= frac, f"{what}: only {inside:.5f} within {atol} abs + {rtol} rel"
+
+
+def inside_fraction(got_u16, want_u16, atol=ATOL, rtol=RTOL) -> float:
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    w = bf16_to_f32(want_u16).astype(np.float64)
+    return float((np.abs(g - w) <= atol + rtol * np.abs(w)).mean())
+
+
+def assert_close_bf16_wide(got_u16, want_u16, atol=ATOL, rtol=RTOL, frac=0.999, what="", floor_u16=None):
+    """Full-width decoders: bf16 rounding of the hidden state (2^-8 relative) flips in a
+    different place on each side and drifts through the layers, so a few logits land just
+    outside the elementwise bound.  Every logit must be within twice the bound, at least
+    `frac` of them within it, and greedy argmax must agree wherever the top-2 margin is clear.
+
+    floor_u16: the oracle's own logits for the same inputs with every fp32 reduction in
+    another order (oracle.reversed_reduction_order), an equally exact forward.  A one-ulp
+    change of an RMSNorm scale flips an element sitting on a bf16 rounding boundary, which
+    moves every projection of that token, so two exact summation orders already disagree on
+    some logits.  The HIP path then has to be as close to the oracle as that reordering:
+    within the bound for at least the lower of `frac` and the floor's fraction less 0.001,
+    and no logit further out than the larger of twice the bound and 1.25 x the floor's
+    worst ratio."""
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    w = bf16_to_f32(want_u16).astype(np.float64)
+    err = np.abs(g - w)
+    bound = atol + rtol * np.abs(w)
+    need, cap, fl = frac, 2.0, None
+    if floor_u16 is not None:
+        fe = np.abs(bf16_to_f32(floor_u16).astype(np.float64) - w) / bound
+        fl = (float((fe <= 1).mean()), float(fe.max()))
+        need, cap = min(frac, fl[0] - 0.001), max(2.0, 1.25 * fl[1])
+    ratio = err / bound
+    assert ratio.max() <= cap, f"{what}: max err {ratio.max():.3f} x the bound (cap {cap:.3f}; reordered oracle {fl})"
+    inside = float((ratio <= 1).mean())
+    assert inside >= need, (f"{what}: only {inside:.5f} within {atol} abs + {rtol} rel (required {need:.5f}; "
+                            f"reordered oracle (inside, max ratio) {fl})")
     ws = np.sort(w, axis=-1)
     clear = (ws[..., -1] - ws[..., -2]) > 4 * 2 * (atol + rtol * np.abs(ws[..., -1]))
     am_g, am_w = np.argmax(g, axis=-1), np.argmax(w, axis=-1)

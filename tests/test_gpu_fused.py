@@ -4,8 +4,8 @@ in one call, and whole speculative steps against the multi-kernel forward."""
 import numpy as np
 import pytest
 
-from tests._common import (ARCH_QWEN3, LLAMA3_8B_1L, QWEN3_4B_2L, assert_close_bf16, assert_close_bf16_wide, cfg,
-                           top2_margin)
+from tests._common import (ARCH_QWEN3, LLAMA3_8B_1L, QWEN3_4B_2L, assert_close_bf16, assert_close_bf16_kv,
+                           assert_close_bf16_wide, cfg, top2_margin)
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -27,20 +27,30 @@ def pair(hip, oracle, c, rows=1, ctx=256):
 def test_fused_verify_matches_oracle(hip, oracle, c):
     gm, gb, om = pair(hip, oracle, c, rows=1, ctx=256)
     assert gb.fused_available()
+    wide = c is not SMALL_D128
+    om_rev = oracle.Model(c, SEED, 256, 1) if wide else None  # the reordered-oracle floor
     rng = np.random.default_rng(5)
     V = c["vocab"]
     toks = rng.integers(0, V, 40).tolist()
     gb.forward([0], [40], toks, want_logits=False)  # 40 tokens: the multi-kernel forward
     om.forward([0], [40], toks, want_logits=False)
+    if wide:
+        with oracle.reversed_reduction_order():
+            om_rev.forward([0], [40], toks, want_logits=False)
     gb.set_fused(2)
-    close = assert_close_bf16 if c is SMALL_D128 else assert_close_bf16_wide
     for width in (6, 1, 8):
         toks = rng.integers(0, V, width).tolist()
-        close(gb.forward([0], [width], toks), om.forward([0], [width], toks), what=f"verify {width}")
+        got, want = gb.forward([0], [width], toks), om.forward([0], [width], toks)
+        if wide:
+            with oracle.reversed_reduction_order():
+                alt = om_rev.forward([0], [width], toks)
+            assert_close_bf16_wide(got, want, what=f"verify {width}", floor_u16=alt)
+        else:
+            assert_close_bf16(got, want, what=f"verify {width}")
     assert gb.kv_len(0) == om.kv_len(0) == 40 + 15
     for layer in range(c["n_layers"]):
         for w in (0, 1):
-            assert_close_bf16(gb.read_kv(layer, 0, w), om.kv(layer, 0, w), what=f"kv {layer} {w}")
+            assert_close_bf16_kv(gb.read_kv(layer, 0, w), om.kv(layer, 0, w), what=f"kv {layer} {w}")
 
 
 def test_fused_equals_multi_kernel_forward(hip):
@@ -76,7 +86,7 @@ def test_fused_long_context_many_blocks(hip, oracle):
         assert_close_bf16(gb.forward([0], [width], toks), om.forward([0], [width], toks), what=f"long verify {width}")
     for layer in range(2):
         for w in (0, 1):
-            assert_close_bf16(gb.read_kv(layer, 0, w), om.kv(layer, 0, w), what=f"kv {layer} {w}")
+            assert_close_bf16_kv(gb.read_kv(layer, 0, w), om.kv(layer, 0, w), what=f"kv {layer} {w}")
 
 
 def test_fused_several_rows(hip, oracle):
@@ -98,23 +108,29 @@ def test_fused_several_rows(hip, oracle):
 
 
 def test_fused_steps_match_multi_kernel_steps(hip):
-    """Greedy speculative steps (drafts from copied spans) with either forward: same tokens."""
+    """Greedy speculative steps (drafts from copied spans) with either forward, replayed from
+    the captured step graph: same tokens.  The prompt's prefill (300 tokens) takes the
+    multi-kernel forward in both; the last step runs with profiling on to show which
+    forward served the verify blocks."""
     from mlxcat_amd.workloads import copy_span_prompt
 
     gm = hip.Model(QWEN3_4B_2L)
     gm.init_synthetic(SEED)
     prompt = copy_span_prompt(9, 300, 151936)
-    outs = []
-    for mode in (2, 0):
+    outs, fused_launches = [], []
+    for mode in (1, 0):
         b = hip.Batch(gm, 1, 512, SPEC)
         b.set_fused(mode)
-        b.insert(0, prompt, 40, hip.make_sampling())
+        b.insert(0, prompt, 200, hip.make_sampling())  # 12 steps emit at most 72 tokens
         toks = []
-        for _ in range(12):
+        for i in range(12):
+            b.set_profiling(i == 11)
             t, n, _f = b.step()
             toks += t[0][: n[0]].tolist()
+        fused_launches.append(b.profile(3)[2])
         outs.append(toks)
     assert outs[0] == outs[1]
+    assert fused_launches[0] >= 1 and fused_launches[1] == 0
 
 
 def test_fused_unavailable_shapes_fall_back(hip):

@@ -132,3 +132,21 @@ def test_rollback_equals_never_verified(oracle):
     a.set_kv_len(0, 12)
     t = [7, 8]
     np.testing.assert_array_equal(a.forward([0], [2], t), b.forward([0], [2], t))
+
+
+def test_reversed_reduction_order_is_a_reordering(oracle):
+    """The reordered reductions (the GPU tests' rounding-noise floor) compute the same sums:
+    fp32 results agree to reordering error, bf16 logits to the elementwise bound."""
+    rng = np.random.default_rng(11)
+    wq, s, b = oracle.gen_linear(SEED, 77, 96, 512)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    y0 = oracle.qmatmul(wq, s, b, x)
+    with oracle.reversed_reduction_order():
+        y1 = oracle.qmatmul(wq, s, b, x)
+    np.testing.assert_allclose(y1, y0, rtol=1e-5, atol=1e-5 * float(np.abs(y0).max()))
+    a, r = oracle.Model(TINY, SEED, 64, 1), oracle.Model(TINY, SEED, 64, 1)
+    toks = rng.integers(0, TINY["vocab"], 12).tolist()
+    la = a.forward([0], [12], toks)
+    with oracle.reversed_reduction_order():
+        lr = r.forward([0], [12], toks)
+    assert_close_bf16(lr, la, what="reversed order")
