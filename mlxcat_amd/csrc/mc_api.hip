@@ -14,6 +14,7 @@
 #include "mc_gemv.hpp"
 #include "mc_kernels.hpp"
 #include "mc_step.hpp"
+#include "mc_xfwd.hpp"
 
 namespace mc {
 
@@ -375,8 +376,14 @@ struct mc_batch {
   FwArgs fw{};                   // fixed arguments; M and the logits flag are set per call
   FwLayer* fw_layers = nullptr;  // device [n_layers]
   unsigned long long* fw_ll = nullptr;
-  unsigned* fw_ctl = nullptr;    // [0] forward-call counter (starts at 1), [1] error word
+  unsigned* fw_ctl = nullptr;    // [0] forward-call counter (starts at 1), [1] error word, [8..15] XCD arrivals
   int fw_grid = 0;
+  // XCD-partitioned persistent forward (mc_xfwd): preferred when available
+  bool xf_ok = false;
+  XArgs xf{};
+  XLayer* xf_layers = nullptr;   // device [n_layers]
+  unsigned long long* xf_ll = nullptr;
+  int xf_grid = 0;
 };
 
 static void batch_free(mc_batch* b) {
@@ -387,7 +394,7 @@ static void batch_free(mc_batch* b) {
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
                   (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
-                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl})
+                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -404,6 +411,84 @@ static int stage_i32(mc_batch* b, size_t n) {
   b->h_i32 = nullptr;
   MC_HIP(hipHostMalloc((void**)&b->h_i32, n * 4, hipHostMallocDefault));
   b->h_i32_n = n;
+  return MC_OK;
+}
+
+// Control words shared by the persistent forwards: call counter (starts at 1), error word,
+// per-XCD arrival counters.
+static int ctl_setup(mc_batch* b) {
+  int rc;
+  if ((rc = dev_zero(&b->fw_ctl, 16))) return rc;
+  const unsigned one = 1u;
+  MC_HIP(hipMemcpy(b->fw_ctl, &one, 4, hipMemcpyHostToDevice));
+  return MC_OK;
+}
+
+static XLin xlin(const QLinear& L) {
+  XLin x;
+  x.qw = L.qw; x.sb = L.sb; x.N = L.N; x.K = L.K; x.NT = L.NT; x.GP = L.GP;
+  return x;
+}
+
+// XCD-partitioned persistent forward (mc_xfwd), when the model, the batch and the device
+// allow it.  Not an error otherwise.
+static int xfwd_setup(mc_batch* b, int kcap) {
+  mc_model* m = b->m;
+  const auto& c = m->cfg;
+  int cus = 0;
+  MC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device));
+  const char* why = nullptr;
+  if (!xfwd_supported(c, b->R, kcap, cus, &why)) return MC_OK;
+  XArgs& a = b->xf;
+  a.bpx = cus / XF_XCD;
+  if (a.bpx & (a.bpx - 1)) return MC_OK;  // the norm reduction pairs lanes by powers of two
+  a.L = c.n_layers;
+  a.H = c.hidden; a.nq = c.n_q_heads; a.nkv = c.n_kv_heads; a.d = c.head_dim; a.I = c.intermediate; a.V = c.vocab;
+  a.eps = c.rms_eps;
+  a.scale = 1.0f / sqrtf((float)a.d);
+  if (!xfwd_plan(a)) return MC_OK;
+  std::vector<XLayer> hl((size_t)c.n_layers);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const auto& L = m->layers[(size_t)l];
+    XLayer& f = hl[(size_t)l];
+    f.qkv = xlin(L.qkv); f.o = xlin(L.o); f.gu = xlin(L.gateup); f.dn = xlin(L.down);
+    f.in_norm = L.in_norm; f.post_norm = L.post_norm; f.q_norm = L.q_norm; f.k_norm = L.k_norm;
+    f.k = b->kv[(size_t)l].k;
+    f.v = b->kv[(size_t)l].v;
+  }
+  int rc;
+  if ((rc = dev_alloc(&b->xf_layers, hl.size()))) return rc;
+  MC_HIP(hipMemcpy(b->xf_layers, hl.data(), hl.size() * sizeof(XLayer), hipMemcpyHostToDevice));
+  const size_t mm = XF_MMAX, X8 = XF_XCD, g = (size_t)(a.nq / a.nkv);
+  a.nch_cap = kcap / 64;
+  const size_t n_x = X8 * mm * a.H / 2, n_ss = X8 * a.bpx * mm, n_qkv = X8 * mm * (g + 2) * a.d / 2,
+               n_rec = X8 * b->R * a.nch_cap * 32 * XF_REC, n_att = X8 * mm * g * a.d / 2, n_part = X8 * mm * a.H,
+               n_act = X8 * mm * a.act_w;
+  if ((rc = dev_zero(&b->xf_ll, 2 * n_x + 2 * n_ss + n_qkv + n_rec + n_att + 2 * n_part + n_act))) return rc;
+  unsigned long long* p = b->xf_ll;
+  a.xl = p; p += n_x;
+  a.x1l = p; p += n_x;
+  a.xss = p; p += n_ss;
+  a.x1ss = p; p += n_ss;
+  a.qkvl = p; p += n_qkv;
+  a.rec = p; p += n_rec;
+  a.attl = p; p += n_att;
+  a.opart = p; p += n_part;
+  a.dpart = p; p += n_part;
+  a.actl = p;
+  a.layers = b->xf_layers;
+  a.embed = xlin(m->embed);
+  a.head = xlin(m->head());
+  a.final_norm = m->final_norm;
+  a.rope_cos = b->rope_cos;
+  a.rope_sin = b->rope_sin;
+  a.cap = kcap;
+  a.R = b->R;
+  a.epoch = b->fw_ctl;
+  a.err = b->fw_ctl + 1;
+  a.xcd_ctr = b->fw_ctl + 8;
+  b->xf_grid = cus;
+  b->xf_ok = true;
   return MC_OK;
 }
 
@@ -448,9 +533,6 @@ static int fused_setup(mc_batch* b, int kcap) {
                n_act = mm * I / 2, n_op = (size_t)oks * mm * H, n_dp = (size_t)dks * mm * H,
                n_ao = (size_t)b->R * nkv * npb * FW_QROWS * d, n_aml = (size_t)b->R * nkv * npb * FW_QROWS * 2;
   if ((rc = dev_zero(&b->fw_ll, n_x + n_xss + n_qkv + n_att + n_act + n_op + n_dp + n_ao + n_aml))) return rc;
-  if ((rc = dev_zero(&b->fw_ctl, 2))) return rc;
-  const unsigned one = 1u;
-  MC_HIP(hipMemcpy(b->fw_ctl, &one, 4, hipMemcpyHostToDevice));
   FwArgs& a = b->fw;
   unsigned long long* p = b->fw_ll;
   a.x = p; p += n_x;
@@ -567,7 +649,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
       batch_free(b);
       return rc;
     }
-    if ((rc = fused_setup(b, kcap))) { batch_free(b); return rc; }
+    if ((rc = ctl_setup(b)) || (rc = fused_setup(b, kcap)) || (rc = xfwd_setup(b, kcap))) { batch_free(b); return rc; }
   }
   if ((rc = dev_zero(&b->logits, (size_t)M * V))) { batch_free(b); return rc; }
 
@@ -668,15 +750,33 @@ static double forward_alg_bytes(const mc_batch* b, int M, bool with_head) {
   return w + ctx * kv_row + (double)M * kv_row;
 }
 
-// Whether this forward runs as the persistent kernel.
+// Whether this forward runs as a persistent kernel (the XCD-partitioned one first).
+static bool use_xf(const mc_batch* b, int M) { return b->xf_ok && b->fused_mode != 0 && M >= 1 && M <= XF_MMAX; }
 static bool use_fused(const mc_batch* b, int M) { return b->fused_ok && b->fused_mode != 0 && M >= 1 && M <= FW_MMAX; }
+
+static int xf_forward(mc_batch* b, int M, bool with_logits) {
+  XArgs a = b->xf;
+  const StepState& s = b->s;
+  a.M = M;
+  a.with_head = with_logits ? 1 : 0;
+  a.slot_tok = s.slot_tok;
+  a.slot_row = s.slot_row;
+  a.row_slot0 = s.row_slot0;
+  a.n_valid = s.n_valid;
+  a.qbase = s.qbase;
+  a.logits = b->logits;
+  a.amax = b->amax;
+  int rc = launch_xfwd(a, b->xf_grid, b->st);
+  if (rc) return rc;
+  return launch_xfwd_epoch(b->fw_ctl, b->fw_ctl + 8, b->st);
+}
 
 // The persistent forward's error word (nonzero: a wait timed out or the unit schedule broke).
 static int fused_check(mc_batch* b) {
-  if (!b->fused_ok) return MC_OK;
+  if (!b->fused_ok && !b->xf_ok) return MC_OK;
   unsigned e = 0;
   MC_HIP(hipMemcpy(&e, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost));
-  if (e) return fail(MC_E_STATE, e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
+  if (e) return fail(MC_E_STATE, e & 4u ? "persistent forward: XCD placement" : e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
   return MC_OK;
 }
 
@@ -725,6 +825,13 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   int rc;
   if (m->fake) {
     if (lgn > 0) return launch_fake_logits(c.arch, s.slot_tok + lg0, lgn, c.vocab, b->logits + (size_t)lg0 * c.vocab, b->st);
+    return MC_OK;
+  }
+  if (use_xf(b, M)) {
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    if ((rc = xf_forward(b, M, lgn > 0))) return rc;
+    if ((rc = prof_end(b, e0, 3, forward_alg_bytes(b, M, lgn > 0)))) return rc;
     return MC_OK;
   }
   if (use_fused(b, M)) {
@@ -1119,11 +1226,13 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
   MC_HIP(hipMemcpyAsync(h + R * K1 + 2 * R, s.nprop, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipMemcpyAsync(h + R * K1 + 3 * R, s.kv_len, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
   h[R * K1 + 4 * R] = 0;
-  if (b->fused_ok) MC_HIP(hipMemcpyAsync(h + R * K1 + 4 * R, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost, b->st));
+  if (b->fused_ok || b->xf_ok) MC_HIP(hipMemcpyAsync(h + R * K1 + 4 * R, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipStreamSynchronize(b->st));
   if (h[R * K1 + 4 * R]) {
     const unsigned e = (unsigned)h[R * K1 + 4 * R];
-    return fail(MC_E_STATE, e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
+    return fail(MC_E_STATE, e & 4u   ? "persistent forward: XCD placement"
+                            : e & 2u ? "persistent forward: unit schedule mismatch"
+                                     : "persistent forward: wait timed out");
   }
   if (out_tokens) memcpy(out_tokens, h, (size_t)R * K1 * 4);
   if (out_counts) memcpy(out_counts, h + R * K1, (size_t)R * 4);
@@ -1167,7 +1276,7 @@ extern "C" int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap) {
 
 extern "C" int mc_batch_set_fused(mc_batch* b, int32_t mode) {
   if (!b || mode < 0 || mode > 2) return fail(MC_E_INVALID, "mc_batch_set_fused: bad argument");
-  if (mode == 2 && !b->fused_ok) return fail(MC_E_STATE, "persistent forward not available for this model / batch");
+  if (mode == 2 && !b->fused_ok && !b->xf_ok) return fail(MC_E_STATE, "persistent forward not available for this model / batch");
   b->fused_mode = mode;
   if (b->graph) {  // the captured step follows the mode it was captured with
     MC_HIP(hipGraphExecDestroy(b->graph));
@@ -1178,7 +1287,7 @@ extern "C" int mc_batch_set_fused(mc_batch* b, int32_t mode) {
   return MC_OK;
 }
 
-extern "C" int mc_batch_fused_available(mc_batch* b) { return b && b->fused_ok ? 1 : 0; }
+extern "C" int mc_batch_fused_available(mc_batch* b) { return b && (b->fused_ok || b->xf_ok) ? 1 : 0; }
 
 extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
   if (!b) return fail(MC_E_INVALID, "null batch");

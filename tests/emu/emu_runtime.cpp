@@ -84,7 +84,7 @@ struct Lane {
   int block = 0, wave = 0, lane = 0;
   bool done = false;
 };
-enum { K_NONE, K_SHFL_F, K_SHFL_I, K_SHFL_U64, K_SHFL_U, K_ANY, K_SYNC, K_MFMA };
+enum { K_NONE, K_SHFL_F, K_SHFL_I, K_SHFL_U64, K_SHFL_U, K_ANY, K_SYNC, K_MFMA, K_MFMA16 };
 struct Wave {
   int kind = K_NONE, arrived = 0;
   unsigned gen = 0;
@@ -108,7 +108,7 @@ ucontext_t sched;
 Idx gdim, bdim;
 int waves_per_block = 4;
 const std::function<void()>* g_body = nullptr;
-const void* g_persistent = nullptr;
+const void* g_persistent[4] = {nullptr, nullptr, nullptr, nullptr};
 
 void yield() { swapcontext(&lanes[(size_t)cur].ctx, &sched); }
 Wave& my_wave() { return waves[(size_t)(lanes[(size_t)cur].block * waves_per_block + lanes[(size_t)cur].wave)]; }
@@ -242,6 +242,45 @@ void mfma_16x16x32_bf16(const void* a, const void* b, const float* c, float* d) 
   memcpy(d, W.D[l], 16);
 }
 
+// v_mfma_f32_16x16x16_bf16: lane l holds A[l % 16][4 (l / 16) + i], B[4 (l / 16) + i][l % 16],
+// C / D [4 (l / 16) + v][l % 16]
+void mfma_16x16x16_bf16(const void* a, const void* b, const float* c, float* d) {
+  Wave& W = my_wave();
+  const int l = my_lane();
+  memcpy(W.A[l], a, 8);
+  memcpy(W.B[l], b, 8);
+  memcpy(W.C[l], c, 16);
+  arrive(W, K_MFMA16, [](Wave& w) {
+    float A[16][16], B[16][16], C[16][16];
+    for (int k = 0; k < 64; ++k)
+      for (int i = 0; i < 4; ++i) {
+        A[k % 16][4 * (k / 16) + i] = bf(w.A[k][i]);
+        B[4 * (k / 16) + i][k % 16] = bf(w.B[k][i]);
+      }
+    for (int k = 0; k < 64; ++k)
+      for (int v = 0; v < 4; ++v) C[4 * (k / 16) + v][k % 16] = w.C[k][v];
+    for (int m = 0; m < 16; ++m)
+      for (int n = 0; n < 16; ++n) {
+        double s = C[m][n];
+        for (int k = 0; k < 16; ++k) s += (double)A[m][k] * (double)B[k][n];
+        C[m][n] = (float)s;
+      }
+    for (int k = 0; k < 64; ++k)
+      for (int v = 0; v < 4; ++v) w.D[k][v] = C[4 * (k / 16) + v][k % 16];
+  });
+  memcpy(d, W.D[l], 16);
+}
+
+void dma(__amdgpu_buffer_rsrc_t r, void* lds, unsigned size, unsigned off) {
+  unsigned char* dst = (unsigned char*)lds + (size_t)my_lane() * size;
+  if ((uint64_t)off + size > r.num) {
+    ++oob_loads;
+    memset(dst, 0, size);
+    return;
+  }
+  memcpy(dst, r.base + off, size);
+}
+
 emu_u32x4 bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
   emu_u32x4 v = {0u, 0u, 0u, 0u};
   if ((uint64_t)off + 16 > r.num) {
@@ -281,7 +320,13 @@ void trace_timeout(int site) {
   fprintf(stderr, "EMU: timeout at wait site %d: block %d wave %d\n", site, L.block, L.wave);
 }
 
-void set_persistent(const void* kernel) { g_persistent = kernel; }
+void set_persistent(const void* kernel) {
+  for (auto& p : g_persistent)
+    if (!p || p == kernel) {
+      p = kernel;
+      return;
+    }
+}
 
 static void lane_main() {
   (*g_body)();
@@ -289,7 +334,7 @@ static void lane_main() {
 }
 
 static std::vector<char*> stack_pool;
-static const size_t STACK = 96 * 1024;
+static const size_t STACK = 256 * 1024;
 
 // run blocks [b0, b1) of the grid to completion; false on a deadlock
 static bool run_blocks(size_t b0, size_t b1, dim3 grid, dim3 block, size_t lds) {
@@ -355,7 +400,11 @@ void run_kernel(const void* kernel, dim3 grid, dim3 block, size_t lds, const std
   const size_t nblocks = (size_t)grid.x * grid.y * grid.z;
   // blocks of ordinary kernels run one at a time (their __shared__ arrays are static);
   // a persistent kernel (its LDS is per block) needs every block live at once
-  const size_t group = kernel == g_persistent ? nblocks : 1;
+  bool persistent = false;
+  for (const void* p : g_persistent) persistent |= p && p == kernel;
+  const size_t group = persistent ? nblocks : 1;
+  if (persistent && getenv("EMU_TRACE_PERSISTENT"))
+    fprintf(stderr, "EMU: persistent launch, %zu blocks of %u threads\n", nblocks, block.x * block.y * block.z);
   for (size_t b0 = 0; b0 < nblocks; b0 += group)
     if (!run_blocks(b0, std::min(nblocks, b0 + group), grid, block, lds)) {
       fprintf(stderr, "EMU: deadlock in a kernel launch\n");

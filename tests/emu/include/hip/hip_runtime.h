@@ -122,6 +122,8 @@ void block_sync();
 void spin_yield();
 unsigned long long clock();
 void mfma_16x16x32_bf16(const void* a, const void* b, const float* c, float* d);
+void mfma_16x16x16_bf16(const void* a, const void* b, const float* c, float* d);
+void dma(__amdgpu_buffer_rsrc_t r, void* lds, unsigned size, unsigned off);
 emu_u32x4 bload16(__amdgpu_buffer_rsrc_t r, unsigned off);
 emu_u32x2 bload8(__amdgpu_buffer_rsrc_t r, unsigned off);
 void bstore8(emu_u32x2 v, __amdgpu_buffer_rsrc_t r, unsigned off);
@@ -208,6 +210,22 @@ inline C emu_mfma6(const V& a, const V& b, const C& c, int, int, int) {
   return d;
 }
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16(...) emu_mfma6(__VA_ARGS__)
+template <class V, class C>
+inline C emu_mfma16(const V& a, const V& b, const C& c, int, int, int) {
+  float cin[4], dout[4];
+  memcpy(cin, &c, 16);
+  emu::mfma_16x16x16_bf16(&a, &b, cin, dout);
+  C d;
+  memcpy(&d, dout, 16);
+  return d;
+}
+#define __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(...) emu_mfma16(__VA_ARGS__)
+// buffer load straight into LDS: lane l writes its size bytes at lds + l size
+inline void emu_dma(__amdgpu_buffer_rsrc_t r, void* lds, unsigned size, unsigned voff, unsigned soff, unsigned off,
+                    unsigned) {
+  emu::dma(r, lds, size, voff + soff + off);
+}
+#define __builtin_amdgcn_raw_ptr_buffer_load_lds(...) emu_dma(__VA_ARGS__)
 
 #define __hip_atomic_load(p, order, scope) __atomic_load_n((p), __ATOMIC_SEQ_CST)
 #define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)

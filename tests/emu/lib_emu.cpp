@@ -7,6 +7,8 @@
 //           the whole K/V against the oracle
 //   case 1: the same model and prefill, verify blocks with the multi-kernel forward
 //   case 2: Qwen3-4B shape (2 layers): 40-token prefill, a 6-token verify (persistent)
+//   case 3: case 0 with 32 q / 8 kv heads, hidden 512 (the XCD-partitioned forward; EMU_CUS=32)
+//   case 4: the case-3 model through mc_step (verify blocks with padding slots; MC_STEP_EAGER=1)
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -16,6 +18,7 @@
 
 #include "../../include/mlxcat_hip.h"
 #include "../../mlxcat_amd/csrc/mc_fused.hpp"
+#include "../../mlxcat_amd/csrc/mc_xfwd.hpp"
 #include "emu.hpp"
 
 extern "C" {
@@ -55,12 +58,19 @@ int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
   emu::set_persistent((const void*)mc::fused_forward_kernel);
+  emu::set_persistent((const void*)mc::xfwd_kernel);
   check(mc_set_device(0), "set_device");
   mc_model_config c{};
   c.arch = 0; c.n_layers = 2; c.hidden = 256; c.n_q_heads = 4; c.n_kv_heads = 2; c.head_dim = 128;
   c.intermediate = 512; c.vocab = 4096; c.tied_embeddings = 1; c.rms_eps = 1e-6f; c.rope_theta = 1e6f;
   if (cs == 2) {
     c.hidden = 2560; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 9728; c.vocab = 151936;
+  }
+  if (cs == 3) {  // smallest shape of the XCD-partitioned forward: 8 kv heads, GQA group 4
+    c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
+  }
+  if (cs == 4) {  // speculative steps through the XCD-partitioned forward: padding slots
+    c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
   const uint64_t SEED = 1234;
   const int ctx = 256, V = c.vocab;
@@ -71,6 +81,40 @@ int main(int argc, char** argv) {
   mc_batch* b = nullptr;
   check(mc_batch_create(m, 1, ctx, 5, &spec, &b), "batch_create");
   printf("persistent forward available: %d\n", mc_batch_fused_available(b));
+  if (cs == 4) {
+    // a prompt without repeats (no drafts: one valid slot of six) and a repeating one
+    // (drafts), each stepped with the persistent forward and with the multi-kernel forward
+    std::vector<std::vector<int32_t>> outs;
+    for (int pass = 0; pass < 4; ++pass) {
+      mc_batch* bb = nullptr;
+      check(mc_batch_create(m, 1, ctx, 5, &spec, &bb), "batch_create");
+      std::vector<int32_t> prompt(48);
+      for (int i = 0; i < 48; ++i) prompt[(size_t)i] = pass < 2 ? (i * 37 + 11) % V : 100 + (i % 8);
+      mc_sampling sp{};
+      sp.reject_token = -1;
+      int32_t first = 0, fin = 0;
+      check(mc_batch_insert(bb, 0, prompt.data(), 48, 24, &sp, &first, &fin), "insert");
+      check(mc_batch_set_fused(bb, pass & 1 ? 0 : 2), "set_fused");  // the prefill took the multi-kernel forward
+      std::vector<int32_t> toks{first};
+      for (int st = 0; st < 6; ++st) {
+        int32_t ot[6], cnt[1], f[1];
+        check(mc_step(bb, nullptr, ot, cnt, f), "step");
+        for (int k = 0; k < cnt[0]; ++k) toks.push_back(ot[k]);
+        if (cnt[0] == 0) break;
+      }
+      printf("pass %d (%s, %s): %zu tokens:", pass, pass < 2 ? "no repeats" : "repeats", pass & 1 ? "multi" : "persistent",
+             toks.size());
+      for (int t : toks) printf(" %d", t);
+      printf("\n");
+      outs.push_back(toks);
+      mc_batch_destroy(bb);
+    }
+    if (outs[0] != outs[1] || outs[2] != outs[3]) printf("note: persistent and multi-kernel steps differ\n");
+    printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
+    if (emu::oob_loads || emu::oob_stores) ++g_bad;
+    printf("%s\n", g_bad ? "FAIL" : "OK");
+    return g_bad ? 1 : 0;
+  }
   or_config oc{c.arch, c.n_layers, c.hidden, c.n_q_heads, c.n_kv_heads, c.head_dim, c.intermediate, c.vocab,
                c.tied_embeddings, c.rms_eps, c.rope_theta, 0, 0, 0};
   or_model* om = or_model_create(&oc, SEED, ctx, 1);
