@@ -381,6 +381,7 @@ struct mc_batch {
   // XCD-partitioned persistent forward (mc_xfwd): preferred when available
   bool xf_ok = false;
   XArgs xf{};
+  XArgs* xf_args = nullptr;      // device copy of xf
   XLayer* xf_layers = nullptr;   // device [n_layers]
   unsigned long long* xf_ll = nullptr;
   int xf_grid = 0;
@@ -394,7 +395,7 @@ static void batch_free(mc_batch* b) {
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
                   (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
-                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll})
+                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll, (void*)b->xf_args})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -489,6 +490,24 @@ static int xfwd_setup(mc_batch* b, int kcap) {
   a.xcd_ctr = b->fw_ctl + 8;
   b->xf_grid = cus;
   b->xf_ok = true;
+  return MC_OK;
+}
+
+// The XCD-partitioned forward's arguments into device memory, once the step state (slot
+// arrays) and the logits buffer exist.
+static int xfwd_finish(mc_batch* b) {
+  if (!b->xf_ok) return MC_OK;
+  XArgs& a = b->xf;
+  a.slot_tok = b->s.slot_tok;
+  a.slot_row = b->s.slot_row;
+  a.row_slot0 = b->s.row_slot0;
+  a.n_valid = b->s.n_valid;
+  a.qbase = b->s.qbase;
+  a.logits = b->logits;
+  a.amax = b->amax;
+  int rc;
+  if ((rc = dev_alloc(&b->xf_args, 1))) return rc;
+  MC_HIP(hipMemcpy(b->xf_args, &a, sizeof(XArgs), hipMemcpyHostToDevice));
   return MC_OK;
 }
 
@@ -691,6 +710,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   }
   if ((rc = stage_i32(b, std::max<size_t>(4096, (size_t)b->hcap + 16)))) { batch_free(b); return rc; }
   MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R + 1) * 4, hipHostMallocDefault));
+  if ((rc = xfwd_finish(b))) { batch_free(b); return rc; }
   *out = b;
   return MC_OK;
 }
@@ -755,18 +775,7 @@ static bool use_xf(const mc_batch* b, int M) { return b->xf_ok && b->fused_mode 
 static bool use_fused(const mc_batch* b, int M) { return b->fused_ok && b->fused_mode != 0 && M >= 1 && M <= FW_MMAX; }
 
 static int xf_forward(mc_batch* b, int M, bool with_logits) {
-  XArgs a = b->xf;
-  const StepState& s = b->s;
-  a.M = M;
-  a.with_head = with_logits ? 1 : 0;
-  a.slot_tok = s.slot_tok;
-  a.slot_row = s.slot_row;
-  a.row_slot0 = s.row_slot0;
-  a.n_valid = s.n_valid;
-  a.qbase = s.qbase;
-  a.logits = b->logits;
-  a.amax = b->amax;
-  int rc = launch_xfwd(a, b->xf_grid, b->st);
+  int rc = launch_xfwd(b->xf_args, b->xf.lds_bytes, M, with_logits ? 1 : 0, b->xf_grid, b->st);
   if (rc) return rc;
   return launch_xfwd_epoch(b->fw_ctl, b->fw_ctl + 8, b->st);
 }

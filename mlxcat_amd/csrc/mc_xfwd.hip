@@ -35,7 +35,15 @@
 // s_waitcnt immediates: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8
 #define XF_WAIT_VM_NF() __builtin_amdgcn_s_waitcnt(((2 * XF_NF) & 0xF) | (((2 * XF_NF) >> 4) << 14) | 0x70 | 0xF00)
 #define XF_WAIT_VM0() __builtin_amdgcn_s_waitcnt(0x0F70)
+// a wave-uniform value in a scalar register (v_readfirstlane with an SGPR result)
+__device__ inline int xf_uniform(int v) {
+  int r;
+  asm volatile("v_readfirstlane_b32 %0, %1" : "=s"(r) : "v"(v));
+  return r;
+}
+#define XF_UNIFORM(v) xf_uniform(v)
 #else
+#define XF_UNIFORM(v) (v)
 #define XF_WAIT_VM_NF() ((void)0)
 #define XF_WAIT_VM0() ((void)0)
 #endif
@@ -65,7 +73,7 @@ enum { TG_X = 0, TG_Q = 1, TG_R = 2, TG_A = 3, TG_O = 4, TG_X1 = 5, TG_U = 6, TG
 enum { OP_Q = 0, OP_O = 1, OP_U = 2, OP_D = 3, OP_HEAD = 4 };
 enum { RX_EMBED = 0, RX_DOWN = 1, RX_O = 2 };
 // control words at LDS offset 0 (ints)
-enum { C_LOADED = 0, C_CONSUMED = 4, C_BAR = 8, C_XI = 9, C_J = 10, C_KVB = 12, C_ROWS = 16 };
+enum { C_LOADED = 0, C_CONSUMED = 8, C_BAR = 16, C_XI = 17, C_J = 18, C_KVB = 20, C_ROWS = 24 };
 // row info (8 ints per row, from C_ROWS)
 enum { RI_T = 0, RI_NV = 1, RI_S0 = 2, RI_NCH = 3, RI_UB = 4 };
 constexpr int CTL_BYTES = (C_ROWS + 8 * XF_MMAX) * 4;
@@ -80,6 +88,21 @@ __device__ inline rsrc_t mk(const void* p, size_t bytes) {
   const int n = bytes > 0x7FFFFFF0ull ? 0x7FFFFFF0 : (int)bytes;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
 }
+// A buffer descriptor from a base and a size that the compiler may not know to be
+// wave-uniform: both go through readfirstlane, so the descriptor lives in scalar registers
+// (a descriptor in vector registers would make every buffer instruction a loop over lanes).
+__device__ inline rsrc_t mk_uniform(const void* p, unsigned bytes) {
+  const unsigned long long u = (unsigned long long)(uintptr_t)p;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+  const unsigned n = __builtin_amdgcn_readfirstlane(bytes);
+  return mk(reinterpret_cast<const void*>((uintptr_t)(((unsigned long long)hi << 32) | lo)), n);
+}
+
+__device__ inline rsrc_t mkd(const void* p, size_t bytes) {
+  return mk_uniform(p, (unsigned)(bytes > 0x7FFFFFF0ull ? 0x7FFFFFF0ull : bytes));
+}
+
 template <int CP>
 __device__ inline u32x4 bld16(rsrc_t r, unsigned off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP); }
 template <int CP>
@@ -140,13 +163,16 @@ struct Ctx {
   int xi, j, gb, G;  // XCD, block within the XCD, block id over the grid, grid
   unsigned ep;
   Ctl cx;
-  int w, lane;       // compute wave / loader index 0..3, lane
+  int w, lane;       // compute wave 0..7 / loader 0..3, lane
   int rc;            // ring chunks consumed (compute) or issued (loader)
   int nb;            // compute-wave barriers passed
+  int M, wh;         // tokens of the launch; 1: the LM head runs
 };
 
 __device__ inline int* ctl_of(unsigned char* lds) { return reinterpret_cast<int*>(lds); }
 __device__ inline const int* rows_of(unsigned char* lds) { return reinterpret_cast<const int*>(lds) + C_ROWS; }
+// field f of row r's info, wave-uniform
+__device__ inline int row_info(const int* ri, int r, int f) { return ri[r * 8 + f]; }
 __device__ inline unsigned char* ring_of(const XArgs& a, unsigned char* lds, int w) {
   return lds + a.o_ring + (size_t)w * a.ring_slots * XF_SLOT;
 }
@@ -280,8 +306,8 @@ __device__ inline bool load_gemv(Loader& Ld, int op, int l) {
   block_tiles(p, c, a.bpx, first, stride, n);
   if (n == 0) return true;
   const XLin& L = p.L;
-  const rsrc_t rq = mk(L.qw, (size_t)L.NT * L.GP * 1024);
-  const rsrc_t rs = mk(L.sb, (size_t)L.NT * L.GP * 32 * 4);
+  const rsrc_t rq = mkd(L.qw, (size_t)L.NT * L.GP * 1024);
+  const rsrc_t rs = mkd(L.sb, (size_t)L.NT * L.GP * 32 * 4);
   for (int gs = 0; gs < n; gs += XF_TG) {
     const int tg = min(XF_TG, n - gs);
     for (int pi = c.w; pi < p.np; pi += XF_NCW) {
@@ -303,9 +329,10 @@ __device__ inline bool load_att(Loader& Ld, int l) {
   const XLayer& Ly = a.layers[l];
   const int* ri = rows_of(c.lds);
   const size_t kvb = (size_t)a.R * a.nkv * a.cap * a.d * 2;
-  const rsrc_t rk = mk(Ly.k, kvb), rv = mk(Ly.v, kvb);
+  const rsrc_t rk = mkd(Ly.k, kvb), rv = mkd(Ly.v, kvb);
   for (int r = 0; r < a.R; ++r) {
-    const int T = ri[r * 8 + RI_T], NV = ri[r * 8 + RI_NV], nch = ri[r * 8 + RI_NCH], ub = ri[r * 8 + RI_UB];
+    const int T = row_info(ri, r, RI_T), NV = row_info(ri, r, RI_NV), nch = row_info(ri, r, RI_NCH),
+              ub = row_info(ri, r, RI_UB);
     for (int ch = 0; ch < nch; ++ch) {
       if ((ub + ch) % a.bpx != c.j) continue;
       const int s = 4 * ch + c.w;
@@ -337,7 +364,7 @@ __device__ void loader_main(const XArgs& a, Ctx& c) {
     ok = load_gemv(Ld, OP_Q, l) && load_att(Ld, l) && load_gemv(Ld, OP_O, l) && load_gemv(Ld, OP_U, l) &&
          load_gemv(Ld, OP_D, l);
   }
-  if (ok && a.with_head) ok = load_gemv(Ld, OP_HEAD, a.L);
+  if (ok && c.wh) ok = load_gemv(Ld, OP_HEAD, a.L);
   XF_WAIT_VM0();
   if (ok) xf_publish(c.lds, c.w, c.rc);
 }
@@ -368,7 +395,7 @@ __device__ inline const unsigned char* ring_slot(const XArgs& a, unsigned char* 
 // ---------------------------------------------------------------------------------------
 __device__ inline bool rx_phase(const XArgs& a, Ctx& c, int l, int kind) {
   const int tid = c.w * 64 + c.lane;
-  const int M = a.M, H = a.H;
+  const int M = c.M, H = a.H;
   const int cb = H / a.bpx, npair = cb / 2, items = M * npair;
   uint16_t* xprev = reinterpret_cast<uint16_t*>(c.lds + a.o_xprev);  // [MMAX][cb]
   float* red = reinterpret_cast<float*>(c.lds + a.o_red);
@@ -376,11 +403,11 @@ __device__ inline bool rx_phase(const XArgs& a, Ctx& c, int l, int kind) {
   const unsigned tout = tagof(c.ep, l, to_x1 ? TG_X1 : TG_X);
   u64* outw = (to_x1 ? a.x1l : a.xl) + (size_t)c.xi * XF_MMAX * (H / 2);
   u64* outs = (to_x1 ? a.x1ss : a.xss) + (size_t)c.xi * a.bpx * XF_MMAX;
-  const rsrc_t ro = mk(outw, (size_t)XF_MMAX * (H / 2) * 8);
-  const rsrc_t ros = mk(outs, (size_t)a.bpx * XF_MMAX * 8);
+  const rsrc_t ro = mkd(outw, (size_t)XF_MMAX * (H / 2) * 8);
+  const rsrc_t ros = mkd(outs, (size_t)a.bpx * XF_MMAX * 8);
   const u64* part = kind == RX_O ? a.opart : a.dpart;
   const unsigned tin = kind == RX_O ? tagof(c.ep, l, TG_O) : tagof(c.ep, l - 1, TG_D);
-  const rsrc_t rp = mk(part, (size_t)XF_XCD * XF_MMAX * H * 8);
+  const rsrc_t rp = mkd(part, (size_t)XF_XCD * XF_MMAX * H * 8);
   for (int it0 = tid; it0 < items; it0 += XF_NCW * 64) {
     const int m = it0 / npair, pp = it0 - m * npair;
     const int col = c.j * cb + 2 * pp;
@@ -455,13 +482,13 @@ constexpr int XQ = 3;  // 16-byte (4-column) input quads per thread, at most (nc
 // Stage the phase input as bf16 rows X[m][0 .. ncol) (RMS-normalised when in.nw).
 __device__ inline bool stage_x(const XArgs& a, Ctx& c, const XIn& in) {
   const int tid = c.w * 64 + c.lane;
-  const int M = a.M;
+  const int M = c.M;
   uint16_t* X = reinterpret_cast<uint16_t*>(c.lds + a.o_x);
-  const rsrc_t rx = mk(in.src, (size_t)XF_MMAX * in.ldw * 8);
+  const rsrc_t rx = mkd(in.src, (size_t)XF_MMAX * in.ldw * 8);
   // norm factors, computed redundantly by every compute wave: lanes take block partials
   float rn[XF_MMAX];
   if (in.nw) {
-    const rsrc_t rs = mk(in.ss, (size_t)a.bpx * XF_MMAX * 8);
+    const rsrc_t rs = mkd(in.ss, (size_t)a.bpx * XF_MMAX * 8);
     const int p = c.lane % a.bpx;
     u32x2 sv[XF_MMAX];
     unsigned pend = 0;
@@ -494,7 +521,7 @@ __device__ inline bool stage_x(const XArgs& a, Ctx& c, const XIn& in) {
   for (int i = 0; i < XQ; ++i)
 #pragma unroll
     for (int m = 0; m < XF_MMAX; ++m)
-      if (tid + 256 * i < nq4 && m < M) pend |= 1u << (i * XF_MMAX + m);
+      if (tid + XF_CT * i < nq4 && m < M) pend |= 1u << (i * XF_MMAX + m);
   int it = 0;
   while (true) {
 #pragma unroll
@@ -502,7 +529,7 @@ __device__ inline bool stage_x(const XArgs& a, Ctx& c, const XIn& in) {
 #pragma unroll
       for (int m = 0; m < XF_MMAX; ++m)
         if (pend >> (i * XF_MMAX + m) & 1u)
-          v[i][m] = bld16<CP_SC1>(rx, (unsigned)(m * in.ldw + 2 * (tid + 256 * i)) * 8u);
+          v[i][m] = bld16<CP_SC1>(rx, (unsigned)(m * in.ldw + 2 * (tid + XF_CT * i)) * 8u);
 #pragma unroll
     for (int i = 0; i < XQ; ++i)
 #pragma unroll
@@ -511,11 +538,11 @@ __device__ inline bool stage_x(const XArgs& a, Ctx& c, const XIn& in) {
     if (!__any(pend != 0u)) break;
     if (spin(c.cx, it)) return false;
   }
-  const rsrc_t rw = mk(in.nw, (size_t)in.ncol * 2);
+  const rsrc_t rw = mkd(in.nw, (size_t)in.ncol * 2);
 #pragma unroll
   for (int i = 0; i < XQ; ++i) {
-    const int cq = tid + 256 * i;
-    if (256 * i >= nq4) break;  // uniform
+    const int cq = tid + XF_CT * i;
+    if (XF_CT * i >= nq4) break;  // uniform
     const bool live = cq < nq4;
     u32x2 wv = {0u, 0u};
     if (in.nw && live) wv = __builtin_amdgcn_raw_buffer_load_b64(rw, (unsigned)cq * 8u, 0, CP_PLAIN);
@@ -572,11 +599,11 @@ __device__ inline XIn gemv_input(const XArgs& a, const Ctx& c, int op, int l) {
 // Epilogue of tile t (local lt) for lanes < 32: acc[v] = token 4c + v of weight row 16 t + r16.
 __device__ inline void gemv_epilogue(const XArgs& a, const Ctx& c, const PD& p, int l, int lt, int t, f32x4 acc) {
   const int lane = c.lane, cq = lane >> 4, r16 = lane & 15;
-  const int M = a.M, H = a.H, g = a.nq / a.nkv;
+  const int M = c.M, H = a.H, g = a.nq / a.nkv;
   const int n = t * 16 + r16;
   if (p.kind == OP_Q) {
     const int ldo = (g + 2) * a.d / 2;
-    const rsrc_t ro = mk(a.qkvl + (size_t)c.xi * XF_MMAX * ldo, (size_t)XF_MMAX * ldo * 8);
+    const rsrc_t ro = mkd(a.qkvl + (size_t)c.xi * XF_MMAX * ldo, (size_t)XF_MMAX * ldo * 8);
     const unsigned tag = tagof(c.ep, l, TG_Q);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -585,7 +612,7 @@ __device__ inline void gemv_epilogue(const XArgs& a, const Ctx& c, const PD& p, 
       if (lane < 32 && !(r16 & 1) && m < M) bst8<CP_PLAIN>(ro, (unsigned)(m * ldo + (lt * 16 + r16) / 2) * 8u, pack2(acc[v], other), tag);
     }
   } else if (p.kind == OP_U) {
-    const rsrc_t ro = mk(a.actl + (size_t)c.xi * XF_MMAX * a.act_w, (size_t)XF_MMAX * a.act_w * 8);
+    const rsrc_t ro = mkd(a.actl + (size_t)c.xi * XF_MMAX * a.act_w, (size_t)XF_MMAX * a.act_w * 8);
     const unsigned tag = tagof(c.ep, l, TG_U);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -599,7 +626,7 @@ __device__ inline void gemv_epilogue(const XArgs& a, const Ctx& c, const PD& p, 
     }
   } else if (p.kind == OP_O || p.kind == OP_D) {
     u64* part = p.kind == OP_O ? a.opart : a.dpart;
-    const rsrc_t ro = mk(part, (size_t)XF_XCD * XF_MMAX * H * 8);
+    const rsrc_t ro = mkd(part, (size_t)XF_XCD * XF_MMAX * H * 8);
     const unsigned tag = tagof(c.ep, l, p.kind == OP_O ? TG_O : TG_D);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -674,7 +701,7 @@ __device__ inline bool gemv_phase(const XArgs& a, Ctx& c, int op, int l) {
   if (n == 0) return true;
   if (!stage_x(a, c, gemv_input(a, c, op, l))) return false;
   const int lane = c.lane, cq = lane >> 4, r16 = lane & 15;
-  const int row = min(r16, a.M - 1);
+  const int row = min(r16, c.M - 1);
   const uint16_t* X = reinterpret_cast<const uint16_t*>(c.lds + a.o_x) + row * a.xst + 8 * cq;
   f32x4* exch = reinterpret_cast<f32x4*>(c.lds + a.o_exch);
   const unsigned char* ring = ring_of(a, c.lds, c.w);
@@ -745,7 +772,7 @@ constexpr int A_END = A_NW + 2 * 128 * 2;
 __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
   const int tid = c.w * 64 + c.lane, lane = c.lane, w = c.w;
   const int* ri = rows_of(c.lds);
-  const int T = ri[r * 8 + RI_T], NV = ri[r * 8 + RI_NV], S0 = ri[r * 8 + RI_S0];
+  const int T = row_info(ri, r, RI_T), NV = row_info(ri, r, RI_NV), S0 = row_info(ri, r, RI_S0);
   const int g = a.nq / a.nkv, d = a.d;
   const XLayer& Ly = a.layers[l];
   unsigned char* st = c.lds + a.o_x;
@@ -760,21 +787,21 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
   // ---- raw q (g heads), k, v rows of the NV new tokens: 32 quads (16 bytes = 2 words) a row ----
   {
     const int ldq = (g + 2) * d / 2;
-    const rsrc_t rq = mk(a.qkvl + (size_t)c.xi * XF_MMAX * ldq, (size_t)XF_MMAX * ldq * 8);
+    const rsrc_t rq = mkd(a.qkvl + (size_t)c.xi * XF_MMAX * ldq, (size_t)XF_MMAX * ldq * 8);
     const unsigned tq = tagof(c.ep, l, TG_Q);
     const int nrow = (g + 2) * NV, np = nrow * 32;
-    constexpr int APP = (48 * 32 + 255) / 256;
+    constexpr int APP = (48 * 32 + XF_CT - 1) / XF_CT;
     u32x4 v[APP];
     unsigned pend = 0;
 #pragma unroll
     for (int q = 0; q < APP; ++q)
-      if (tid + 256 * q < np) pend |= 1u << q;
+      if (tid + XF_CT * q < np) pend |= 1u << q;
     int it = 0;
     while (true) {
 #pragma unroll
       for (int q = 0; q < APP; ++q)
         if (pend >> q & 1u) {
-          const int p = tid + 256 * q, rr = p >> 5, pw = p & 31;
+          const int p = tid + XF_CT * q, rr = p >> 5, pw = p & 31;
           const int hs = rr / NV, jj = rr - hs * NV;
           v[q] = bld16<CP_SC1>(rq, (unsigned)((S0 + jj) * ldq + hs * (d / 2) + 2 * pw) * 8u);
         }
@@ -786,15 +813,15 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
     }
 #pragma unroll
     for (int q = 0; q < APP; ++q) {
-      const int p = tid + 256 * q;
+      const int p = tid + XF_CT * q;
       if (p < np) *reinterpret_cast<u32x2*>(raw + (p >> 5) * 128 + 4 * (p & 31)) = (u32x2){v[q].x, v[q].z};
     }
-    for (int i2 = tid; i2 < NV * 64; i2 += 256) {
+    for (int i2 = tid; i2 < NV * 64; i2 += XF_CT) {
       const int jj = i2 >> 6, e = i2 & 63;
       cs[i2] = a.rope_cos[(size_t)(T + jj) * 64 + e];
       sn[i2] = a.rope_sin[(size_t)(T + jj) * 64 + e];
     }
-    for (int i2 = tid; i2 < 256; i2 += 256) {
+    for (int i2 = tid; i2 < 256; i2 += XF_CT) {
       const uint16_t* src = i2 < 128 ? Ly.q_norm : Ly.k_norm;
       nwl[i2] = src ? src[i2 & 127] : (uint16_t)0;
     }
@@ -848,7 +875,7 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
   if (!cw_barrier(c)) return false;
   // ---- this wave's 16-key sub-block: patch in the new keys, append them to the cache ----
   const int s = 4 * ch + w;
-  const bool valid = 16 * s < T + NV;
+  const bool valid = w < XF_G && 16 * s < T + NV;
   if (valid) {
     if (!ring_wait(c, c.rc + 8)) return false;
     const int lo = max(16 * s, T), hi = min(16 * s + 16, T + NV);
@@ -869,10 +896,10 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
       }
     }
   }
-  if (lane == 0) kvb[w] = valid ? c.rc : -1;
+  if (lane == 0 && w < XF_G) kvb[w] = valid ? c.rc : -1;
   if (!cw_barrier(c)) return false;
-  // ---- GQA head gq = w against the chunk's 64 keys ----
-  {
+  // ---- GQA head gq = w (waves 0..3) against the chunk's 64 keys ----
+  if (w < XF_G) {
     const int gq = w, n = lane & 15, c4 = lane >> 4;
     const int qrow = min(n, NV - 1);
     bf16x8 qv[4];
@@ -942,7 +969,7 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
     }
     // record (o unnormalised, max, sum) of query n of head gq: lane holds o[16 db + 4 c4 + v]
     const size_t rec0 = ((((size_t)c.xi * a.R + r) * a.nch_cap + ch) * 32 + gq * 8 + n) * XF_REC;
-    const rsrc_t rr = mk(a.rec, (size_t)XF_XCD * a.R * a.nch_cap * 32 * XF_REC * 8);
+    const rsrc_t rr = mkd(a.rec, (size_t)XF_XCD * a.R * a.nch_cap * 32 * XF_REC * 8);
     const unsigned tr = tagof(c.ep, l, TG_R);
     if (n < NV) {
 #pragma unroll
@@ -965,7 +992,7 @@ __device__ inline bool att_unit(const XArgs& a, Ctx& c, int l, int r, int ch) {
 __device__ inline bool att_phase(const XArgs& a, Ctx& c, int l) {
   const int* ri = rows_of(c.lds);
   for (int r = 0; r < a.R; ++r) {
-    const int nch = ri[r * 8 + RI_NCH], ub = ri[r * 8 + RI_UB];
+    const int nch = row_info(ri, r, RI_NCH), ub = row_info(ri, r, RI_UB);
     for (int ch = 0; ch < nch; ++ch) {
       if ((ub + ch) % a.bpx != c.j) continue;
       if (!att_unit(a, c, l, r, ch)) return false;
@@ -982,19 +1009,19 @@ __device__ inline bool comb_phase(const XArgs& a, Ctx& c, int l) {
   const int* ri = rows_of(c.lds);
   const int lane = c.lane, w = c.w, g = a.nq / a.nkv;
   const unsigned tr = tagof(c.ep, l, TG_R), ta = tagof(c.ep, l, TG_A);
-  const rsrc_t rr = mk(a.rec, (size_t)XF_XCD * a.R * a.nch_cap * 32 * XF_REC * 8);
+  const rsrc_t rr = mkd(a.rec, (size_t)XF_XCD * a.R * a.nch_cap * 32 * XF_REC * 8);
   const int ldo = g * a.d / 2;
-  const rsrc_t ro = mk(a.attl + (size_t)c.xi * XF_MMAX * ldo, (size_t)XF_MMAX * ldo * 8);
+  const rsrc_t ro = mkd(a.attl + (size_t)c.xi * XF_MMAX * ldo, (size_t)XF_MMAX * ldo * 8);
   f32x4* cm = reinterpret_cast<f32x4*>(c.lds + a.o_cm);  // [4 waves][64 lanes] (max, sum, o0, o1)
   constexpr int CPW = 9;  // chunks a wave merges per pass
-  for (int u = c.j; u < a.M * g; u += a.bpx) {
+  for (int u = c.j; u < c.M * g; u += a.bpx) {
     const int s = u / g, gq = u - s * g;
     const int r = a.slot_row[s];
     int jj = -1, nch = 0;
     if (r >= 0 && r < a.R) {
-      jj = s - ri[r * 8 + RI_S0];
-      nch = ri[r * 8 + RI_NCH];
-      if (jj < 0 || jj >= ri[r * 8 + RI_NV]) jj = -1;
+      jj = s - row_info(ri, r, RI_S0);
+      nch = row_info(ri, r, RI_NCH);
+      if (jj < 0 || jj >= row_info(ri, r, RI_NV)) jj = -1;
     }
     float mx = -INFINITY, ls = 0.f, o0 = 0.f, o1 = 0.f;
     if (jj >= 0) {
@@ -1054,7 +1081,7 @@ __device__ inline bool comb_phase(const XArgs& a, Ctx& c, int l) {
       const float inv = L2 > 0.f ? 1.0f / L2 : 0.f;
       bst8<CP_PLAIN>(ro, (unsigned)(s * ldo + gq * (a.d / 2) + lane) * 8u, pack2(O0 * inv, O1 * inv), ta);
     }
-    if (u + a.bpx < a.M * g && !cw_barrier(c)) return false;  // cm is rewritten by the next unit
+    if (u + a.bpx < c.M * g && !cw_barrier(c)) return false;  // cm is rewritten by the next unit
   }
   return true;
 }
@@ -1071,7 +1098,7 @@ __device__ void compute_main(const XArgs& a, Ctx& c) {
     if (!gemv_phase(a, c, OP_D, l)) return;
   }
   if (!rx_phase(a, c, a.L, RX_DOWN)) return;
-  if (a.with_head) gemv_phase(a, c, OP_HEAD, a.L);
+  if (c.wh) gemv_phase(a, c, OP_HEAD, a.L);
 }
 
 }  // namespace
@@ -1079,8 +1106,9 @@ __device__ void compute_main(const XArgs& a, Ctx& c) {
 // ---------------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(XF_THREADS) xfwd_kernel(XArgs a) {
+__global__ void __launch_bounds__(XF_THREADS) xfwd_kernel(const XArgs* __restrict__ ap, int M, int with_head) {
   MC_DYN_LDS(lds);
+  const XArgs& a = *ap;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   int* ctl = ctl_of(lds);
   if (tid == 0) {
@@ -1112,20 +1140,25 @@ __global__ void __launch_bounds__(XF_THREADS) xfwd_kernel(XArgs a) {
     }
   }
   __syncthreads();
+  // values read back from memory are wave-uniform: say so (readfirstlane), so that every
+  // address derived from them stays scalar (a buffer descriptor the compiler must assume to
+  // vary across lanes turns each buffer instruction into a loop over lanes)
   Ctx c;
   c.lds = lds;
-  c.xi = ctl[C_XI];
-  c.j = ctl[C_J];
+  c.xi = XF_UNIFORM(ctl[C_XI]);
+  c.j = XF_UNIFORM(ctl[C_J]);
   if (c.xi < 0 || c.xi >= XF_XCD) return;
   c.gb = c.xi * a.bpx + c.j;
   c.G = XF_XCD * a.bpx;
-  c.ep = *a.epoch;
+  c.ep = (unsigned)XF_UNIFORM((int)*a.epoch);
   c.cx.t0 = wall_clock64();
   c.cx.err = a.err;
-  c.w = w & 3;
+  c.w = w < XF_NCW ? w : w - XF_NCW;
   c.lane = lane;
   c.rc = 0;
   c.nb = 0;
+  c.M = M;
+  c.wh = with_head;
   if (w >= XF_NCW) loader_main(a, c);
   else compute_main(a, c);
 }
@@ -1145,9 +1178,9 @@ bool xfwd_supported(const mc_model_config& c, int R, int cap, int cus, const cha
   const int g = c.n_kv_heads > 0 ? c.n_q_heads / c.n_kv_heads : 0;
   if (cus % XF_XCD || cus < XF_XCD) r = "CU count is not a multiple of the XCD count";
   else if (c.n_kv_heads != XF_XCD) r = "kv heads != XCD count";
-  else if (g != XF_NCW || g * c.n_kv_heads != c.n_q_heads) r = "GQA group != 4";
+  else if (g != XF_G || g * c.n_kv_heads != c.n_q_heads) r = "GQA group != 4";
   else if (c.head_dim != 128) r = "head_dim != 128";
-  else if (c.hidden % 256 || c.hidden > 256 * 4 * XQ || (c.hidden / (cus / XF_XCD)) % 2) r = "hidden size";
+  else if (c.hidden % 256 || c.hidden > XF_CT * 4 * XQ || (c.hidden / (cus / XF_XCD)) % 2) r = "hidden size";
   else if (c.intermediate % 128) r = "intermediate not a multiple of 128";
   else if (c.n_layers < 1 || c.n_layers > 62) r = "layer count";
   else if (c.n_experts > 0) r = "mixture of experts";
@@ -1165,7 +1198,7 @@ bool xfwd_plan(XArgs& a) {
   for (int x = 0; x < XF_XCD; ++x) mx = std::max(mx, a.pdn[x + 1] - a.pdn[x]);
   a.act_w = mx * 64;
   const int kst = std::max(std::max(H, g * a.d), 128 * mx);
-  if (kst > 256 * 4 * XQ) return false;  // staging: XQ quads of 4 columns per compute thread
+  if (kst > XF_CT * 4 * XQ) return false;  // staging: XQ quads of 4 columns per compute thread
   const int cb = H / a.bpx;
   auto al = [](int x) { return (x + 15) & ~15; };
   int o = CTL_BYTES;
@@ -1180,18 +1213,18 @@ bool xfwd_plan(XArgs& a) {
   a.o_ring = o;
   const int limit = 160 * 1024;
   a.ring_slots = (limit - o) / (XF_NCW * XF_SLOT);
-  if (a.ring_slots < XF_NF + 2) return false;
+  if (a.ring_slots < XF_NF + 2) return false;  // and at least the 8 chunks of an attention sub-block
   a.lds_bytes = o + a.ring_slots * XF_NCW * XF_SLOT;
   return true;
 }
 
-int launch_xfwd(const XArgs& a, int grid, hipStream_t st) {
+int launch_xfwd(const XArgs* dev_args, int lds_bytes, int M, int with_head, int grid, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
     MC_HIP(hipFuncSetAttribute((const void*)xfwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     attr = true;
   }
-  hipLaunchKernelGGL(xfwd_kernel, dim3(grid), dim3(XF_THREADS), a.lds_bytes, st, a);
+  hipLaunchKernelGGL(xfwd_kernel, dim3(grid), dim3(XF_THREADS), lds_bytes, st, dev_args, M, with_head);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }

@@ -10,9 +10,9 @@
 // tag naming the forward call, layer and phase); a consumer polls exactly the words it
 // needs until every tag matches.
 //
-// A block has 8 waves: waves 0..3 compute, waves 4..7 are loaders.  Loader 4 + w streams
-// the weights (and cached K/V) that compute wave w will consume, in consumption order,
-// into an LDS ring with direct-to-LDS buffer loads, as far ahead as the ring allows.  So
+// A block has 8 waves: waves 0..3 compute, waves 4..7 are loaders.  Loader 4 + i streams
+// the weights (and cached K/V) that compute wave i will consume, in consumption order,
+// into its LDS ring with direct-to-LDS buffer loads, as far ahead as the ring allows.  So
 // the HBM stream never waits for a phase's inputs, and a compute wave's own vector-memory
 // counter holds only its polls (never a prefetch it would have to drain first).
 #pragma once
@@ -21,8 +21,11 @@
 namespace mc {
 
 constexpr int XF_XCD = 8;        // XCDs; XCD i owns kv head i
-constexpr int XF_NCW = 4;        // compute waves per block (= GQA group size)
-constexpr int XF_THREADS = 512;  // 4 compute + 4 loader waves
+constexpr int XF_NCW = 4;        // compute waves per block (one per SIMD)
+constexpr int XF_NLW = 4;        // loader waves per block; loader i feeds compute wave i
+constexpr int XF_G = 4;          // GQA group size: compute waves 0..3 take one q head each in attention
+constexpr int XF_CT = XF_NCW * 64;                 // compute threads
+constexpr int XF_THREADS = (XF_NCW + XF_NLW) * 64;  // 512
 constexpr int XF_MMAX = 8;       // tokens per launch, at most
 constexpr int XF_TG = 5;         // output tiles per compute group
 constexpr int XF_SLOT = 1152;    // ring slot: 1 KiB of weights or K/V + 128 B of scales/biases
@@ -59,7 +62,7 @@ struct XArgs {
   const float* rope_cos = nullptr;  // [ctx][d / 2]
   const float* rope_sin = nullptr;
   int cap = 0;                      // cache position stride
-  int R = 0, M = 0;
+  int R = 0;
   int bpx = 32;                     // blocks per XCD (grid = 8 bpx)
   int pdn[XF_XCD + 1] = {0};        // down-projection group-pair split over the XCDs
   int act_w = 0;                    // words per token row of the local activation slice
@@ -82,7 +85,6 @@ struct XArgs {
   unsigned long long* opart = nullptr;  // [8][MMAX][H] o-projection partials (f32, read by every XCD)
   unsigned long long* actl = nullptr;   // [8][MMAX][act_w]
   unsigned long long* dpart = nullptr;  // [8][MMAX][H] down-projection partials
-  int with_head = 1;
   uint16_t* logits = nullptr;           // [M][V]
   unsigned long long* amax = nullptr;   // [M][head.NT] tile argmax keys (mc_gemv's encoding)
   const unsigned* epoch = nullptr;      // forward-call counter (bumped after each launch)
@@ -93,13 +95,15 @@ struct XArgs {
   int lds_bytes = 0;
 };
 
-__global__ void xfwd_kernel(XArgs a);
+// The fixed arguments live in device memory (scalar loads; a by-value argument struct whose
+// address is taken is copied to scratch); the token count and the head flag vary per launch.
+__global__ void xfwd_kernel(const XArgs* __restrict__ args, int M, int with_head);
 
 // Whether the XCD-partitioned forward serves this model and batch (why: the reason if not).
 bool xfwd_supported(const mc_model_config& c, int R, int cap, int cus, const char** why);
 // Fill the LDS layout and the down-projection split of a; false if the shape does not fit.
 bool xfwd_plan(XArgs& a);
-int launch_xfwd(const XArgs& a, int grid, hipStream_t st);
+int launch_xfwd(const XArgs* dev_args, int lds_bytes, int M, int with_head, int grid, hipStream_t st);
 // epoch += 1 and the per-XCD arrival counters back to zero
 int launch_xfwd_epoch(unsigned* epoch, unsigned* xcd_ctr, hipStream_t st);
 

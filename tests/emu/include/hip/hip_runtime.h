@@ -183,6 +183,7 @@ using std::max;
 using std::min;
 
 #define __builtin_amdgcn_s_sleep(n) emu::spin_yield()
+#define __builtin_amdgcn_readfirstlane(x) (x)  // every lane of a wave holds the same value here
 #define __builtin_amdgcn_s_waitcnt(n) emu::wave_sync()
 #define __builtin_amdgcn_wave_barrier() emu::wave_sync()
 #define __builtin_amdgcn_s_barrier() emu::block_sync()
