@@ -201,4 +201,13 @@ __host__ __device__ inline uint32_t synth_scale_bias(uint64_t base, int n, int G
 }
 inline uint64_t synth_base(uint64_t seed, uint64_t tid) { return mix64(seed ^ mix64(tid)); }
 
+// Sum over the 8 lanes (l & ~7) .. + 7, the same value in each: DPP quad swaps (xor 1, xor 2),
+// then the half-row mirror (lane 7 - l of the other quad holds the other quad's sum).
+__device__ inline float sum8_lanes(float v) {
+  v += __uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0xB1, 0xF, 0xF, false));
+  v += __uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0x4E, 0xF, 0xF, false));
+  v += __uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0, (int)__float_as_uint(v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 }  // namespace mc

@@ -287,13 +287,17 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
     }
   }
   const int xtotal = Mr * cpr;
+  // chunk i of the K-range's activations is row i / cpr, chunk i % cpr: the quotient by a
+  // multiply-high with ceil(2^32 / cpr), exact for i * cpr < 2^32 (i < 16 MT cpr <= 20480)
+  const unsigned cpr_magic = 0xFFFFFFFFu / (unsigned)cpr + 1u;
+  auto row_of = [&](int i) { return (int)__umulhi((unsigned)i, cpr_magic); };
   u32x4 xv[XCH];
 #pragma unroll
   for (int q = 0; q < XCH; ++q) {
     const int i = tid + 256 * q;
     xv[q] = (u32x4){0u, 0u, 0u, 0u};
     if (i < xtotal) {
-      const int m = i / cpr, ch = i - m * cpr;
+      const int m = row_of(i), ch = i - m * cpr;
       if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
     }
   }
@@ -321,46 +325,61 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
     }
     lds_barrier();
   }
+  // Staging in phases over SB chunks at a time (LDS reads, normalise, LDS stores, group sums,
+  // cross-lane sums, xsum stores) so that the LDS latencies of the chunks overlap.
+  constexpr int SB = 4;
   auto stage = [&](int base) {
 #pragma unroll
-    for (int q = 0; q < XCH; ++q) {
-      const int i = base + tid + 256 * q;
-      if (i < xtotal) {
-        const int m = i / cpr, ch = i - m * cpr;
-        u32x4 v = xv[q];
-        if (a.norm_w) {
-          // bf16((x * r) * w): the rounding of a standalone RMSNorm
-          const float r = rs[m];
-          const u32x4 w = *reinterpret_cast<const u32x4*>(wl + ch * 8);
+    for (int q0 = 0; q0 < XCH; q0 += SB) {
+      int mm[SB], cc[SB];
+      bool in[SB];
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const int i = base + tid + 256 * (q0 + j);
+        in[j] = i < xtotal;
+        mm[j] = row_of(i);
+        cc[j] = i - mm[j] * cpr;
+      }
+      if (a.norm_w) {
+        float rr[SB];
+        u32x4 ww[SB];
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          rr[j] = in[j] ? rs[mm[j]] : 0.f;
+          ww[j] = in[j] ? *reinterpret_cast<const u32x4*>(wl + cc[j] * 8) : (u32x4){0u, 0u, 0u, 0u};
+        }
+        // bf16((x * r) * w): the rounding of a standalone RMSNorm
+#pragma unroll
+        for (int j = 0; j < SB; ++j)
 #pragma unroll
           for (int h = 0; h < 4; ++h) {
-            const float lo = (bf16_to_f32((uint16_t)(v[h] & 0xFFFFu)) * r) * bf16_to_f32((uint16_t)(w[h] & 0xFFFFu));
-            const float hi = (bf16_to_f32((uint16_t)(v[h] >> 16)) * r) * bf16_to_f32((uint16_t)(w[h] >> 16));
+            u32x4& v = xv[q0 + j];
+            const float lo = (__uint_as_float(v[h] << 16) * rr[j]) * __uint_as_float(ww[j][h] << 16);
+            const float hi = (__uint_as_float(v[h] & 0xFFFF0000u) * rr[j]) * __uint_as_float(ww[j][h] & 0xFFFF0000u);
             v[h] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
           }
-        }
-        *reinterpret_cast<u32x4*>(xl + m * XS + ch * 8) = v;
       }
+#pragma unroll
+      for (int j = 0; j < SB; ++j)
+        if (in[j]) *reinterpret_cast<u32x4*>(xl + mm[j] * XS + cc[j] * 8) = xv[q0 + j];
       // group sum of X: the 8 chunks of a 64-wide group sit in 8 consecutive lanes (cpr is
-      // a multiple of 16), reduced in a fixed butterfly order
-      float gs = 0.f;
-      if (i < xtotal) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(xl + (i / cpr) * XS + (i % cpr) * 8);
-        float q0 = 0.f, q1 = 0.f;
+      // a multiple of 16), reduced in a fixed order
+      float gs[SB];
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-          q0 += bf16_to_f32((uint16_t)(v[h] & 0xFFFFu));
-          q1 += bf16_to_f32((uint16_t)(v[h] >> 16));
+          s0 += __uint_as_float(xv[q0 + j][h] << 16);
+          s1 += __uint_as_float(xv[q0 + j][h] & 0xFFFF0000u);
         }
-        gs = q0 + q1;
+        gs[j] = in[j] ? s0 + s1 : 0.f;
       }
-      gs += __shfl_xor(gs, 1);
-      gs += __shfl_xor(gs, 2);
-      gs += __shfl_xor(gs, 4);
-      if (i < xtotal && (i & 7) == 0) {
-        const int m = i / cpr, gl = (i % cpr) >> 3;
-        xsum[gl * 16 * MT + m] = gs;
-      }
+#pragma unroll
+      for (int j = 0; j < SB; ++j) gs[j] = sum8_lanes(gs[j]);
+#pragma unroll
+      for (int j = 0; j < SB; ++j)
+        if (in[j] && (cc[j] & 7) == 0) xsum[(cc[j] >> 3) * 16 * MT + mm[j]] = gs[j];
     }
   };
   stage(0);
@@ -371,7 +390,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
         const int i = base + tid + 256 * q;
         xv[q] = (u32x4){0u, 0u, 0u, 0u};
         if (i < xtotal) {
-          const int m = i / cpr, ch = i - m * cpr;
+          const int m = row_of(i), ch = i - m * cpr;
           if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
         }
       }
@@ -380,10 +399,8 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
     __builtin_amdgcn_s_waitcnt(0);  // leave no load of this branch pending at the merge
   }
   // token rows Mr .. 16 MT - 1 of xsum: zero (their MFMA columns are finite and never stored)
-  for (int i = tid; i < (16 * MT - Mr) * ng; i += 256) {
-    const int m = Mr + i % (16 * MT - Mr), gl = i / (16 * MT - Mr);
-    xsum[gl * 16 * MT + m] = 0.f;
-  }
+  if (lane < 16 * MT - Mr)
+    for (int gl = wave; gl < ng; gl += GEMV_WAVES) xsum[gl * 16 * MT + Mr + lane] = 0.f;
   lds_barrier();
 
   // ---- 4. units: prefetch the next, compute this one, reduce (waves take turns) ----

@@ -148,6 +148,7 @@ void launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t, A... args)
 #define gridDim (*emu::g_gdim)
 #define blockDim (*emu::g_bdim)
 
+inline unsigned __umulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long long)a * b) >> 32); }
 inline float __shfl_xor(float v, int mask, int width = 64) {
   (void)width;
   return emu::shfl_xor_f(v, mask);
@@ -161,6 +162,17 @@ inline unsigned long long __shfl_xor(unsigned long long v, int mask, int width =
   return emu::shfl_xor_u64(v, mask);
 }
 inline unsigned __shfl(unsigned v, int src) { return emu::shfl_u(v, src); }
+// DPP moves used by the kernels: quad_perm (ctrl < 0x100) and the half-row mirror (0x141),
+// every row and bank enabled
+inline int emu_dpp(int src, int ctrl) {
+  const int l = (int)(threadIdx.x & 63);
+  int s;
+  if (ctrl < 0x100) s = (l & ~3) | ((ctrl >> (2 * (l & 3))) & 3);
+  else if (ctrl == 0x141) s = (l & ~7) | (7 - (l & 7));
+  else abort();
+  return (int)emu::shfl_u((unsigned)src, s);
+}
+#define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((src), (ctrl))
 inline int __any(int pred) { return emu::any(pred); }
 inline void __syncthreads() { emu::block_sync(); }
 inline unsigned long long wall_clock64() { return emu::clock(); }
