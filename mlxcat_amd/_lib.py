@@ -171,21 +171,24 @@ class Model:
     def init_synthetic(self, seed: int) -> None:
         _check(load().mc_model_init_synthetic(self.h, seed))
 
-    def _lshape(self, which: int):
+    def _lshape(self, which: int, expert: int = -1):
         c = self.cfg
         H, d, nq, nkv, I = c.hidden, c.head_dim, c.n_q_heads, c.n_kv_heads, c.intermediate
+        if expert >= 0:  # a Qwen3-MoE expert's gate / up / down
+            I = c.moe_intermediate
         return {W_Q: (nq * d, H), W_K: (nkv * d, H), W_V: (nkv * d, H), W_O: (H, nq * d), W_GATE: (I, H),
-                W_UP: (I, H), W_DOWN: (H, I), W_EMBED: (c.vocab, H), W_LM_HEAD: (c.vocab, H)}[which]
+                W_UP: (I, H), W_DOWN: (H, I), W_ROUTER: (c.n_experts, H), W_EMBED: (c.vocab, H),
+                W_LM_HEAD: (c.vocab, H)}[which]
 
     def set_linear(self, layer: int, which: int, wq, scales, biases, expert: int = -1) -> None:
-        N, K = self._lshape(which)
+        N, K = self._lshape(which, expert)
         wq = np.ascontiguousarray(wq, dtype=np.uint32).reshape(N, K // 8)
         s = np.ascontiguousarray(scales, dtype=np.uint16).reshape(N, K // 64)
         b = np.ascontiguousarray(biases, dtype=np.uint16).reshape(N, K // 64)
         _check(load().mc_model_set_linear(self.h, layer, which, expert, _p(wq), _p(s), _p(b)))
 
     def get_linear(self, layer: int, which: int, expert: int = -1):
-        N, K = self._lshape(which)
+        N, K = self._lshape(which, expert)
         wq = np.zeros((N, K // 8), dtype=np.uint32)
         s = np.zeros((N, K // 64), dtype=np.uint16)
         b = np.zeros((N, K // 64), dtype=np.uint16)

@@ -80,6 +80,9 @@ struct mc_model {
   bool fake = false;
   struct Layer {
     QLinear qkv, o, gateup, down;
+    // Qwen3-MoE: the router and every expert's interleaved gate/up and down (expert e's
+    // tiles at e * qw_words() / e * sb_words() of the N x K shape the linear records)
+    QLinear router, egu, edn;
     uint16_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   };
   std::vector<Layer> layers;
@@ -87,7 +90,27 @@ struct mc_model {
   uint16_t* final_norm = nullptr;
   hipStream_t st = nullptr;
   const QLinear& head() const { return cfg.tied_embeddings ? embed : lm_head; }
+  bool moe() const { return cfg.arch == MC_ARCH_QWEN3_MOE; }
 };
+
+// Expert e of a linear holding every expert's tiles.
+static QLinear expert_view(const QLinear& all, int e) {
+  QLinear v = all;
+  v.qw = all.qw + (size_t)e * all.qw_words();
+  v.sb = all.sb + (size_t)e * all.sb_words();
+  return v;
+}
+
+static int experts_alloc(QLinear* L, int E, int N, int K) {
+  if (N <= 0 || K <= 0 || K % 64) return fail(MC_E_INVALID, "expert linear: K must be a positive multiple of 64");
+  L->N = N;
+  L->K = K;
+  L->NT = (N + 15) / 16;
+  L->GP = (K + 127) / 128;
+  int rc = dev_zero(&L->qw, L->qw_words() * (size_t)E);
+  if (rc) return rc;
+  return dev_zero(&L->sb, L->sb_words() * (size_t)E);
+}
 
 extern "C" const char* mc_last_error(void) { return g_err.c_str(); }
 
@@ -122,7 +145,7 @@ extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
     *out = m;
     return MC_OK;
   }
-  if (c.arch != MC_ARCH_QWEN3 && c.arch != MC_ARCH_LLAMA) {
+  if (c.arch != MC_ARCH_QWEN3 && c.arch != MC_ARCH_LLAMA && c.arch != MC_ARCH_QWEN3_MOE) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: architecture not supported by this build");
   }
@@ -131,6 +154,14 @@ extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: unsupported shape");
   }
+  if (c.arch == MC_ARCH_QWEN3_MOE &&
+      (c.n_experts < 1 || c.n_experts > 256 || c.n_experts_per_tok < 1 || c.n_experts_per_tok > 8 ||
+       c.n_experts_per_tok > c.n_experts || c.moe_intermediate <= 0 || c.moe_intermediate % 64 ||
+       c.moe_intermediate > 2560 || c.hidden > 2560)) {
+    delete m;
+    return fail(MC_E_INVALID, "mc_model_create: unsupported MoE shape (<= 256 experts, top-k <= 8, hidden and expert "
+                              "width multiples of 64, <= 2560)");
+  }
   int rc = MC_OK;
   MC_HIP(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
@@ -138,10 +169,16 @@ extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
   for (auto& L : m->layers) {
     if ((rc = qlinear_alloc(&L.qkv, (nq + 2 * nkv) * d, H))) break;
     if ((rc = qlinear_alloc(&L.o, H, nq * d))) break;
-    if ((rc = qlinear_alloc(&L.gateup, 2 * I, H))) break;
-    if ((rc = qlinear_alloc(&L.down, H, I))) break;
+    if (c.arch == MC_ARCH_QWEN3_MOE) {
+      if ((rc = qlinear_alloc(&L.router, c.n_experts, H))) break;
+      if ((rc = experts_alloc(&L.egu, c.n_experts, 2 * c.moe_intermediate, H))) break;
+      if ((rc = experts_alloc(&L.edn, c.n_experts, H, c.moe_intermediate))) break;
+    } else {
+      if ((rc = qlinear_alloc(&L.gateup, 2 * I, H))) break;
+      if ((rc = qlinear_alloc(&L.down, H, I))) break;
+    }
     if ((rc = norm_ones(&L.in_norm, H)) || (rc = norm_ones(&L.post_norm, H))) break;
-    if (c.arch == MC_ARCH_QWEN3) {
+    if (c.arch == MC_ARCH_QWEN3 || c.arch == MC_ARCH_QWEN3_MOE) {
       if ((rc = norm_ones(&L.q_norm, d)) || (rc = norm_ones(&L.k_norm, d))) break;
     }
   }
@@ -165,6 +202,9 @@ extern "C" void mc_model_destroy(mc_model* m) {
     qlinear_free(&L.o);
     qlinear_free(&L.gateup);
     qlinear_free(&L.down);
+    qlinear_free(&L.router);
+    qlinear_free(&L.egu);
+    qlinear_free(&L.edn);
     for (uint16_t* p : {L.in_norm, L.post_norm, L.q_norm, L.k_norm})
       if (p) (void)hipFree(p);
   }
@@ -176,24 +216,37 @@ extern "C" void mc_model_destroy(mc_model* m) {
 }
 
 // Where an MLX tensor lands inside the fused tile tensors: (linear, row offset, row stride, rows).
-static int linear_slot(mc_model* m, int layer, int which, QLinear** L, int* off, int* stride, int* rows, int* K) {
+// expert >= 0 names one expert's gate / up / down of a Qwen3-MoE layer.
+static int linear_slot(mc_model* m, int layer, int which, int expert, QLinear* L, int* off, int* stride, int* rows, int* K) {
   const auto& c = m->cfg;
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
-  if (which == MC_W_EMBED) { *L = &m->embed; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK; }
+  if (expert >= 0 && (!m->moe() || expert >= c.n_experts)) return fail(MC_E_INVALID, "no such expert");
+  if (which == MC_W_EMBED) { *L = m->embed; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK; }
   if (which == MC_W_LM_HEAD) {
     if (c.tied_embeddings) return fail(MC_E_INVALID, "tied model has no separate lm_head");
-    *L = &m->lm_head; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK;
+    *L = m->lm_head; *off = 0; *stride = 1; *rows = c.vocab; *K = H; return MC_OK;
   }
   if (layer < 0 || layer >= c.n_layers) return fail(MC_E_INVALID, "layer out of range");
   auto& Ly = m->layers[(size_t)layer];
+  if (m->moe() && (which == MC_W_GATE || which == MC_W_UP || which == MC_W_DOWN)) {
+    if (expert < 0) return fail(MC_E_INVALID, "MoE layer: gate / up / down need an expert index");
+    const int MI = c.moe_intermediate;
+    if (which == MC_W_DOWN) { *L = expert_view(Ly.edn, expert); *off = 0; *stride = 1; *rows = H; *K = MI; return MC_OK; }
+    *L = expert_view(Ly.egu, expert); *off = which == MC_W_UP ? 1 : 0; *stride = 2; *rows = MI; *K = H;
+    return MC_OK;
+  }
+  if (expert >= 0) return fail(MC_E_INVALID, "only gate / up / down have experts");
   switch (which) {
-    case MC_W_Q: *L = &Ly.qkv; *off = 0; *stride = 1; *rows = nq * d; *K = H; return MC_OK;
-    case MC_W_K: *L = &Ly.qkv; *off = nq * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
-    case MC_W_V: *L = &Ly.qkv; *off = (nq + nkv) * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
-    case MC_W_O: *L = &Ly.o; *off = 0; *stride = 1; *rows = H; *K = nq * d; return MC_OK;
-    case MC_W_GATE: *L = &Ly.gateup; *off = 0; *stride = 2; *rows = I; *K = H; return MC_OK;
-    case MC_W_UP: *L = &Ly.gateup; *off = 1; *stride = 2; *rows = I; *K = H; return MC_OK;
-    case MC_W_DOWN: *L = &Ly.down; *off = 0; *stride = 1; *rows = H; *K = I; return MC_OK;
+    case MC_W_Q: *L = Ly.qkv; *off = 0; *stride = 1; *rows = nq * d; *K = H; return MC_OK;
+    case MC_W_K: *L = Ly.qkv; *off = nq * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
+    case MC_W_V: *L = Ly.qkv; *off = (nq + nkv) * d; *stride = 1; *rows = nkv * d; *K = H; return MC_OK;
+    case MC_W_O: *L = Ly.o; *off = 0; *stride = 1; *rows = H; *K = nq * d; return MC_OK;
+    case MC_W_GATE: *L = Ly.gateup; *off = 0; *stride = 2; *rows = I; *K = H; return MC_OK;
+    case MC_W_UP: *L = Ly.gateup; *off = 1; *stride = 2; *rows = I; *K = H; return MC_OK;
+    case MC_W_DOWN: *L = Ly.down; *off = 0; *stride = 1; *rows = H; *K = I; return MC_OK;
+    case MC_W_ROUTER:
+      if (!m->moe()) return fail(MC_E_INVALID, "dense model has no router");
+      *L = Ly.router; *off = 0; *stride = 1; *rows = c.n_experts; *K = H; return MC_OK;
     default: return fail(MC_E_INVALID, "unknown linear slot");
   }
 }
@@ -202,11 +255,10 @@ extern "C" int mc_model_set_linear(mc_model* m, int32_t layer, int32_t which, in
                                    const uint16_t* scales, const uint16_t* biases) {
   if (!m || !wq || !scales || !biases) return fail(MC_E_INVALID, "mc_model_set_linear: null argument");
   if (m->fake) return fail(MC_E_STATE, "fake model has no weights");
-  if (expert >= 0) return fail(MC_E_INVALID, "MoE experts are not supported by this build");
   MC_HIP(hipSetDevice(m->device));
-  QLinear* L;
+  QLinear L;
   int off, stride, rows, K;
-  int rc = linear_slot(m, layer, which, &L, &off, &stride, &rows, &K);
+  int rc = linear_slot(m, layer, which, expert, &L, &off, &stride, &rows, &K);
   if (rc) return rc;
   uint32_t* dq;
   uint16_t *ds, *db;
@@ -218,7 +270,7 @@ extern "C" int mc_model_set_linear(mc_model* m, int32_t layer, int32_t which, in
   if (e == hipSuccess) e = hipMemcpy(ds, scales, ns * 2, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(db, biases, ns * 2, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    rc = qlinear_repack(*L, off, stride, rows, dq, ds, db, m->st);
+    rc = qlinear_repack(L, off, stride, rows, dq, ds, db, m->st);
     if (!rc) e = hipStreamSynchronize(m->st);
   }
   (void)hipFree(dq);
@@ -232,11 +284,10 @@ extern "C" int mc_model_get_linear(mc_model* m, int32_t layer, int32_t which, in
                                    uint16_t* scales, uint16_t* biases) {
   if (!m || !wq || !scales || !biases) return fail(MC_E_INVALID, "mc_model_get_linear: null argument");
   if (m->fake) return fail(MC_E_STATE, "fake model has no weights");
-  if (expert >= 0) return fail(MC_E_INVALID, "MoE experts are not supported by this build");
   MC_HIP(hipSetDevice(m->device));
-  QLinear* L;
+  QLinear L;
   int off, stride, rows, K;
-  int rc = linear_slot(m, layer, which, &L, &off, &stride, &rows, &K);
+  int rc = linear_slot(m, layer, which, expert, &L, &off, &stride, &rows, &K);
   if (rc) return rc;
   uint32_t* dq;
   uint16_t *ds, *db;
@@ -244,7 +295,7 @@ extern "C" int mc_model_get_linear(mc_model* m, int32_t layer, int32_t which, in
   if ((rc = dev_alloc(&dq, nw))) return rc;
   if ((rc = dev_alloc(&ds, ns))) { (void)hipFree(dq); return rc; }
   if ((rc = dev_alloc(&db, ns))) { (void)hipFree(dq); (void)hipFree(ds); return rc; }
-  rc = qlinear_export(*L, off, stride, rows, dq, ds, db, m->st);
+  rc = qlinear_export(L, off, stride, rows, dq, ds, db, m->st);
   hipError_t e = hipSuccess;
   if (!rc) e = hipStreamSynchronize(m->st);
   if (!rc && e == hipSuccess) e = hipMemcpy(wq, dq, nw * 4, hipMemcpyDeviceToHost);
@@ -308,9 +359,20 @@ extern "C" int mc_model_init_synthetic(mc_model* m, uint64_t seed) {
     if ((rc = qlinear_synth(L.qkv, nq * d, 1, nkv * d, synth_base(seed, tensor_id(l, T_K)), -7, m->st))) return rc;
     if ((rc = qlinear_synth(L.qkv, (nq + nkv) * d, 1, nkv * d, synth_base(seed, tensor_id(l, T_V)), -7, m->st))) return rc;
     if ((rc = qlinear_synth(L.o, 0, 1, H, synth_base(seed, tensor_id(l, T_O)), -7, m->st))) return rc;
-    if ((rc = qlinear_synth(L.gateup, 0, 2, I, synth_base(seed, tensor_id(l, T_GATE)), -7, m->st))) return rc;
-    if ((rc = qlinear_synth(L.gateup, 1, 2, I, synth_base(seed, tensor_id(l, T_UP)), -7, m->st))) return rc;
-    if ((rc = qlinear_synth(L.down, 0, 1, H, synth_base(seed, tensor_id(l, T_DOWN)), -7, m->st))) return rc;
+    if (m->moe()) {
+      const int MI = c.moe_intermediate;
+      if ((rc = qlinear_synth(L.router, 0, 1, c.n_experts, synth_base(seed, tensor_id(l, T_ROUTER)), -7, m->st))) return rc;
+      for (int e = 0; e < c.n_experts; ++e) {
+        const QLinear gu = expert_view(L.egu, e), dn = expert_view(L.edn, e);
+        if ((rc = qlinear_synth(gu, 0, 2, MI, synth_base(seed, expert_tensor_id(l, e, T_GATE)), -7, m->st))) return rc;
+        if ((rc = qlinear_synth(gu, 1, 2, MI, synth_base(seed, expert_tensor_id(l, e, T_UP)), -7, m->st))) return rc;
+        if ((rc = qlinear_synth(dn, 0, 1, H, synth_base(seed, expert_tensor_id(l, e, T_DOWN)), -7, m->st))) return rc;
+      }
+    } else {
+      if ((rc = qlinear_synth(L.gateup, 0, 2, I, synth_base(seed, tensor_id(l, T_GATE)), -7, m->st))) return rc;
+      if ((rc = qlinear_synth(L.gateup, 1, 2, I, synth_base(seed, tensor_id(l, T_UP)), -7, m->st))) return rc;
+      if ((rc = qlinear_synth(L.down, 0, 1, H, synth_base(seed, tensor_id(l, T_DOWN)), -7, m->st))) return rc;
+    }
     auto w = synth_norm(seed, tensor_id(l, T_IN_NORM), H);
     MC_HIP(hipMemcpy(L.in_norm, w.data(), (size_t)H * 2, hipMemcpyHostToDevice));
     w = synth_norm(seed, tensor_id(l, T_POST_NORM), H);
@@ -350,6 +412,11 @@ struct mc_batch {
   int gemv_cnt_n = 0;
   float* ssq = nullptr;  // [Mmax][hidden / 16]: per-tile sums of squares of the residual stream
   unsigned long long* amax = nullptr;  // [Mmax][vocab tiles]: greedy argmax partials of the head
+  // Qwen3-MoE: normalised rows, router logits, routing, per-pair expert outputs
+  uint16_t *moe_xn = nullptr, *moe_logits = nullptr, *moe_act = nullptr;
+  float* moe_out = nullptr;   // [Mmax * TK][hidden] down-projection output of each pair
+  int32_t* moe_i32 = nullptr; // n_active per layer [L] | act_e [E] | off [E + 1] | pairs, sel [Mmax * TK]
+  float* moe_wts = nullptr;   // [Mmax * TK]
   AttnWork aw{};
   StepState s;
   void* scratch = nullptr;  // one allocation for the small StepState arrays
@@ -395,7 +462,9 @@ static void batch_free(mc_batch* b) {
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
                   (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
-                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll, (void*)b->xf_args})
+                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll, (void*)b->xf_args,
+                  (void*)b->moe_xn, (void*)b->moe_logits, (void*)b->moe_act, (void*)b->moe_out, (void*)b->moe_i32,
+                  (void*)b->moe_wts})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -652,7 +721,9 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
       }
       maxnt = std::max(maxnt, L.NT);
     };
-    for (auto& L : m->layers) { acc_plan(L.qkv); acc_plan(L.o); acc_plan(L.gateup); acc_plan(L.down); }
+    for (auto& L : m->layers)
+      for (const QLinear* q : {&L.qkv, &L.o, &L.gateup, &L.down, &L.router})
+        if (q->N > 0) acc_plan(*q);
     acc_plan(m->head());
     b->gemv_part_n = part;
     b->gemv_cnt_n = maxnt;
@@ -667,6 +738,15 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
         (rc = dev_alloc(&b->aw.part_ml, (size_t)M * nq * b->aw.nchunk * 2))) {
       batch_free(b);
       return rc;
+    }
+    if (m->moe()) {
+      const size_t E = (size_t)c.n_experts, P = (size_t)M * c.n_experts_per_tok;
+      if ((rc = dev_zero(&b->moe_xn, (size_t)M * H)) || (rc = dev_zero(&b->moe_logits, (size_t)M * E)) ||
+          (rc = dev_zero(&b->moe_act, P * c.moe_intermediate)) || (rc = dev_zero(&b->moe_out, P * H)) ||
+          (rc = dev_zero(&b->moe_i32, (size_t)c.n_layers + 2 * E + 1 + 2 * P)) || (rc = dev_zero(&b->moe_wts, P))) {
+        batch_free(b);
+        return rc;
+      }
     }
     if ((rc = ctl_setup(b)) || (rc = fused_setup(b, kcap)) || (rc = xfwd_setup(b, kcap))) { batch_free(b); return rc; }
   }
@@ -825,6 +905,65 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
   return MC_OK;
 }
 
+// Routing of layer l: its touched-expert count stays at moe_i32[l] (read back for the
+// byte count of a profiled step); the lists are rewritten by every layer.
+static MoeRoute moe_route_of(mc_batch* b, int l) {
+  const auto& c = b->m->cfg;
+  const size_t E = (size_t)c.n_experts, P = (size_t)b->Mmax * c.n_experts_per_tok;
+  int32_t* p = b->moe_i32;
+  MoeRoute rt;
+  rt.n_active = p + l;
+  p += c.n_layers;
+  rt.act_e = p; p += E;
+  rt.off = p; p += E + 1;
+  rt.pairs = p; p += P;
+  rt.sel = p;
+  rt.wts = b->moe_wts;
+  return rt;
+}
+
+// Blocks per touched expert: about 8 tiles each.
+static int moe_blocks_per_expert(const QLinear& L) { return std::max(1, std::min(L.NT, (L.NT + 7) / 8)); }
+
+// The Qwen3-MoE MLP of layer l over M tokens (Qwen3MoeSparseMoeBlock, EXTERNAL to the
+// reference tree): post-attention RMSNorm, router, softmax top-k with renormalised weights,
+// each touched expert's SwiGLU MLP over its tokens, the weighted sum added to the residual.
+static int moe_mlp(mc_batch* b, int l, int M) {
+  const mc_model* m = b->m;
+  const auto& c = m->cfg;
+  const auto& L = m->layers[(size_t)l];
+  const int H = c.hidden, E = c.n_experts, TK = c.n_experts_per_tok, MI = c.moe_intermediate;
+  int rc;
+  for (int m0 = 0; m0 < M; m0 += 64) {
+    const int mc = std::min(64, M - m0);
+    uint16_t* x = b->x + (size_t)m0 * H;
+    if ((rc = launch_rows_rmsnorm(x, L.post_norm, mc, H, c.rms_eps, b->moe_xn, b->st))) return rc;
+    if ((rc = run_gemv(b, L.router, b->moe_xn, H, nullptr, b->moe_logits, E, mc, EPI_STORE))) return rc;
+    const MoeRoute rt = moe_route_of(b, l);
+    if ((rc = launch_moe_route(b->moe_logits, mc, E, TK, rt, b->st))) return rc;
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    MoeGemvArgs a;
+    a.rt = rt;
+    a.max_active = std::min(E, mc * TK);
+    a.qw = L.egu.qw; a.sb = L.egu.sb; a.qw_es = L.egu.qw_words(); a.sb_es = L.egu.sb_words();
+    a.N = L.egu.N; a.K = L.egu.K; a.NT = L.egu.NT; a.GP = L.egu.GP;
+    a.x = b->moe_xn; a.ldx = H; a.x_div = TK;
+    a.epi = EPI_SWIGLU; a.y = b->moe_act; a.ldy = MI;
+    a.nb = moe_blocks_per_expert(L.egu);
+    if ((rc = moe_gemv_launch(a, b->st))) return rc;
+    a.qw = L.edn.qw; a.sb = L.edn.sb; a.qw_es = L.edn.qw_words(); a.sb_es = L.edn.sb_words();
+    a.N = L.edn.N; a.K = L.edn.K; a.NT = L.edn.NT; a.GP = L.edn.GP;
+    a.x = b->moe_act; a.ldx = MI; a.x_div = 1;
+    a.epi = EPI_STORE; a.y = nullptr; a.yf = b->moe_out; a.ldy = H;
+    a.nb = moe_blocks_per_expert(L.edn);
+    if ((rc = moe_gemv_launch(a, b->st))) return rc;
+    if ((rc = prof_end(b, e0, 0, 0.0))) return rc;
+    if ((rc = launch_moe_combine(x, b->moe_out, rt.wts, mc, TK, H, b->ssq + (size_t)m0 * (H / 16), b->st))) return rc;
+  }
+  return MC_OK;
+}
+
 // Forward over M slots already described in the StepState slot arrays.  Logits are
 // produced for slots [lg0, lg0 + lgn) into b->logits rows [lg0, lg0 + lgn).
 static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
@@ -868,6 +1007,10 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
       return rc;
     if ((rc = prof_end(b, e0, 1, 0.0))) return rc;
     if ((rc = run_gemv(b, L.o, b->att, nq * d, nullptr, b->x, H, M, EPI_RESIDUAL))) return rc;
+    if (m->moe()) {
+      if ((rc = moe_mlp(b, l, M))) return rc;
+      continue;
+    }
     if ((rc = run_gemv(b, L.gateup, b->x, H, L.post_norm, b->act, I, M, EPI_SWIGLU))) return rc;
     if ((rc = run_gemv(b, L.down, b->act, I, nullptr, b->x, H, M, EPI_RESIDUAL))) return rc;
   }

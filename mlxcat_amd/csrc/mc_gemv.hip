@@ -574,9 +574,299 @@ static int setup_mt() {
   return MC_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// grouped (MoE) GEMV
+// ---------------------------------------------------------------------------------------
+constexpr int MOE_MAX_GP = 20;  // K <= 2560
+
+__host__ __device__ constexpr size_t moe_lds_bytes(int GP) {
+  return (size_t)16 * xrow_stride(GP) * 2 + (size_t)16 * 2 * GP * 4 + (size_t)2 * GEMV_WAVES * 64 * 16;
+}
+
+// Block (slot, jb): touched expert act_e[slot], tiles jb, jb + nb, ... with the full K range.
+// The expert's pairs are taken 16 at a time (one m-tile); for each such group the block
+// stages the pairs' input rows and streams its tiles, the next tile's weights in flight
+// while the current one is computed.
+template <int D>
+__global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
+  MC_DYN_LDS(smem);
+  const int slot = blockIdx.x / a.nb, jb = blockIdx.x - slot * a.nb;
+  if (slot >= *a.rt.n_active || jb >= a.NT) return;  // uniform over the block
+  const int e = a.rt.act_e[slot];
+  const int p0 = a.rt.off[slot], np = a.rt.off[slot + 1] - p0;
+  const int GP = a.GP, XS = xrow_stride(GP), cpr = GP * 16, ng = 2 * GP;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                      // [16][XS]
+  float* xsum = reinterpret_cast<float*>(smem + (size_t)16 * XS * 2);    // [2 GP][16]
+  float* red = xsum + 16 * ng;                                           // [2][4][64][4]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane >> 4, r16 = lane & 15;
+  GemvArgs g;  // the expert's weights, for load_unit
+  g.qw = a.qw + (size_t)e * a.qw_es;
+  g.sb = a.sb + (size_t)e * a.sb_es;
+  g.GP = GP;
+  const unsigned cpr_magic = 0xFFFFFFFFu / (unsigned)cpr + 1u;
+  const uint32_t mask = a.dq_mask;
+  uint32_t magic;
+  MC_TO_VGPR(magic, a.dq_magic);
+  for (int q0 = 0; q0 < np; q0 += 16) {
+    const int Mr = min(16, np - q0);
+    int step = 0;  // weight buffer and reduction buffer parity, reduction wave
+    // the first tile's weights, then the pairs' input rows into LDS
+    WBuf<D> wa, wb;
+    load_unit<D>(wa, g, jb, 0, GP, wave, lane, r16);
+    for (int i0 = 0; i0 < Mr * cpr; i0 += 256 * 4) {
+      u32x4 v[4];
+      int mm[4], cc[4];
+      bool in[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + tid + 256 * j;
+        in[j] = i < Mr * cpr;
+        mm[j] = (int)__umulhi((unsigned)i, cpr_magic);
+        cc[j] = i - mm[j] * cpr;
+        v[j] = (u32x4){0u, 0u, 0u, 0u};
+        if (in[j] && cc[j] * 8 < a.K) {
+          const int row = a.rt.pairs[p0 + q0 + mm[j]] / a.x_div;
+          v[j] = *reinterpret_cast<const u32x4*>(a.x + (size_t)row * a.ldx + cc[j] * 8);
+        }
+      }
+      float gs[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (in[j]) *reinterpret_cast<u32x4*>(xl + mm[j] * XS + cc[j] * 8) = v[j];
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          s0 += __uint_as_float(v[j][h] << 16);
+          s1 += __uint_as_float(v[j][h] & 0xFFFF0000u);
+        }
+        gs[j] = in[j] ? s0 + s1 : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gs[j] = sum8_lanes(gs[j]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (in[j] && (cc[j] & 7) == 0) xsum[(cc[j] >> 3) * 16 + mm[j]] = gs[j];
+    }
+    if (lane < 16 - Mr)
+      for (int gl = wave; gl < ng; gl += GEMV_WAVES) xsum[gl * 16 + Mr + lane] = 0.f;
+    lds_barrier();
+    for (int t = jb; t < a.NT; t += a.nb, ++step) {
+      const bool odd = (step & 1) != 0;
+      WBuf<D>& cur = odd ? wb : wa;
+      WBuf<D>& nxt = odd ? wa : wb;
+      const int tn = t + a.nb < a.NT ? t + a.nb : t;  // the last tile re-reads itself
+      load_unit<D>(nxt, g, tn, 0, GP, wave, lane, r16);
+      f32x4 acc[1];
+      compute_unit<1, D>(acc, cur, xl, xsum, XS, Mr, GP, wave, c, r16, mask, magic);
+      float* rb = red + (size_t)(step & 1) * GEMV_WAVES * 64 * 4;
+      *reinterpret_cast<f32x4*>(rb + (wave * 64 + lane) * 4) = acc[0];
+      lds_barrier();
+      if (wave == (step & 3)) {
+        reduce_waves<1>(acc, rb, lane);
+        const int n = t * 16 + r16;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 4 * c + v;
+          const bool live = m < Mr;
+          const int pr = live ? a.rt.pairs[p0 + q0 + m] : 0;
+          if (a.epi == EPI_SWIGLU) {
+            const float up = __shfl_xor(acc[0][v], 1);
+            if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)pr * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[0][v]) * up);
+          } else if (live && n < a.N) {
+            a.yf[(size_t)pr * a.ldy + n] = acc[0][v];
+          }
+        }
+      }
+    }
+    // the staged rows are rewritten by the next group: every wave is past its last tile
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+  }
+}
+
+int moe_gemv_launch(const MoeGemvArgs& a, hipStream_t st) {
+  if (a.K % 64 || a.GP != (a.K + 127) / 128 || a.NT != (a.N + 15) / 16 || a.GP > MOE_MAX_GP)
+    return fail(MC_E_INVALID, "moe gemv: shape (K must be a multiple of 64, at most 2560)");
+  if (a.nb < 1 || a.max_active < 1 || !a.rt.n_active || !a.rt.act_e || !a.rt.off || !a.rt.pairs || a.x_div < 1)
+    return fail(MC_E_INVALID, "moe gemv: routing arguments");
+  if ((a.epi == EPI_SWIGLU && (!a.y || a.N % 2)) || (a.epi == EPI_STORE && !a.yf) ||
+      (a.epi != EPI_SWIGLU && a.epi != EPI_STORE))
+    return fail(MC_E_INVALID, "moe gemv: epilogue");
+  const size_t lds = moe_lds_bytes(a.GP);
+  const dim3 grid((unsigned)(a.max_active * a.nb));
+  switch ((a.GP + GEMV_WAVES - 1) / GEMV_WAVES) {
+    case 1: hipLaunchKernelGGL(moe_gemv_kernel<1>, grid, dim3(256), lds, st, a); break;
+    case 2: hipLaunchKernelGGL(moe_gemv_kernel<2>, grid, dim3(256), lds, st, a); break;
+    case 3: hipLaunchKernelGGL(moe_gemv_kernel<3>, grid, dim3(256), lds, st, a); break;
+    case 4: hipLaunchKernelGGL(moe_gemv_kernel<4>, grid, dim3(256), lds, st, a); break;
+    default: hipLaunchKernelGGL(moe_gemv_kernel<5>, grid, dim3(256), lds, st, a); break;
+  }
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// One block per row: sum of squares in a fixed order (thread partials, then a tree over
+// the block), then bf16((x * r) * w).
+__global__ void __launch_bounds__(256) rows_rmsnorm_kernel(const uint16_t* x, const uint16_t* w, int H, float eps,
+                                                           uint16_t* xn) {
+  __shared__ float part[256];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* xr = x + (size_t)t * H;
+  float q = 0.f;
+  for (int k = tid; k < H; k += 256) {
+    const float v = bf16_to_f32(xr[k]);
+    q += v * v;
+  }
+  part[tid] = q;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) part[tid] += part[tid + s];
+    __syncthreads();
+  }
+  const float r = 1.0f / sqrtf(part[0] / (float)H + eps);
+  for (int k = tid; k < H; k += 256) xn[(size_t)t * H + k] = f32_to_bf16((bf16_to_f32(xr[k]) * r) * bf16_to_f32(w[k]));
+}
+
+int launch_rows_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, float eps, uint16_t* xn, hipStream_t st) {
+  if (M < 1) return MC_OK;
+  hipLaunchKernelGGL(rows_rmsnorm_kernel, dim3(M), dim3(256), 0, st, x, w, H, eps, xn);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// One block.  Wave w routes tokens w, w + 4, ...: the E <= 256 bf16 logits (4 per lane),
+// softmax in fp32, TK rounds of the largest remaining probability (lowest expert on
+// ties), weights renormalised over the selection in selection order.  Then thread e
+// counts expert e's pairs, thread 0 forms the touched-expert list and offsets, and
+// thread e writes its pairs in ascending order.
+__global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, int M, int E, int TK, MoeRoute rt) {
+  __shared__ int cnt[256], slot_of[256];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int t = wave; t < M; t += 4) {
+    float p[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane + 64 * j;
+      p[j] = ex < E ? bf16_to_f32(logits[(size_t)t * E + ex]) : -INFINITY;
+      mx = fmaxf(mx, p[j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float den = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[j] = lane + 64 * j < E ? expf(p[j] - mx) : 0.f;
+      den += p[j];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] /= den;
+    unsigned taken = 0u;  // bit j: expert lane + 64 j already selected
+    float wsel[8], wsum = 0.f;
+    int esel[8];
+    for (int kk = 0; kk < TK; ++kk) {
+      // key: probability bits (non-negative floats order as unsigned) over the inverted index
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ex = lane + 64 * j;
+        if (ex < E && !((taken >> j) & 1u)) {
+          const unsigned long long k = ((unsigned long long)__float_as_uint(p[j]) << 32) | (0xFFFFFFFFu - (unsigned)ex);
+          best = k > best ? k : best;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long ot = __shfl_xor(best, o);
+        best = ot > best ? ot : best;
+      }
+      const int ex = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
+      if ((ex & 63) == lane) taken |= 1u << (ex >> 6);
+      esel[kk] = ex;
+      wsel[kk] = __uint_as_float((unsigned)(best >> 32));
+      wsum += wsel[kk];
+    }
+    if (lane == 0)
+      for (int kk = 0; kk < TK; ++kk) {
+        rt.sel[t * TK + kk] = esel[kk];
+        rt.wts[t * TK + kk] = wsel[kk] / wsum;
+      }
+  }
+  __syncthreads();
+  const int P = M * TK;
+  if (tid < E) {
+    int n = 0;
+    for (int i = 0; i < P; ++i) n += rt.sel[i] == tid;
+    cnt[tid] = n;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int na = 0, o = 0;
+    for (int ex = 0; ex < E; ++ex) {
+      slot_of[ex] = -1;
+      if (cnt[ex] == 0) continue;
+      slot_of[ex] = na;
+      rt.act_e[na] = ex;
+      rt.off[na] = o;
+      o += cnt[ex];
+      ++na;
+    }
+    rt.off[na] = o;
+    *rt.n_active = na;
+  }
+  __syncthreads();
+  if (tid < E && slot_of[tid] >= 0) {
+    int o = rt.off[slot_of[tid]];
+    for (int i = 0; i < P; ++i)
+      if (rt.sel[i] == tid) rt.pairs[o++] = i;
+  }
+}
+
+int launch_moe_route(const uint16_t* logits, int M, int E, int TK, const MoeRoute& rt, hipStream_t st) {
+  if (E < 1 || E > 256 || TK < 1 || TK > 8 || TK > E) return fail(MC_E_INVALID, "moe route: experts (<= 256) / top-k (<= 8)");
+  if (M < 1) return MC_OK;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, st, logits, M, E, TK, rt);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// Block per (row, 256 columns): thread n sums its pairs' outputs in kk order, adds the
+// residual; 16-lane groups form the tile sums of squares of the new row.
+__global__ void __launch_bounds__(256) moe_combine_kernel(uint16_t* x, const float* yd, const float* wts, int TK, int H,
+                                                          float* ss) {
+  const int t = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+  float q = 0.f;
+  if (n < H) {
+    float mo = 0.f;
+    for (int kk = 0; kk < TK; ++kk) mo += wts[t * TK + kk] * yd[((size_t)t * TK + kk) * H + n];
+    uint16_t* xp = x + (size_t)t * H + n;
+    const uint16_t h = f32_to_bf16(bf16_to_f32(*xp) + mo);
+    *xp = h;
+    const float r = bf16_to_f32(h);
+    q = r * r;
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
+  if (n < H && (threadIdx.x & 15) == 0) ss[(size_t)t * (H / 16) + n / 16] = q;
+}
+
+int launch_moe_combine(uint16_t* x, const float* yd, const float* wts, int M, int TK, int H, float* ss, hipStream_t st) {
+  if (H % 16) return fail(MC_E_INVALID, "moe combine: hidden size must be a multiple of 16");
+  if (M < 1) return MC_OK;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((H + 255) / 256, M), dim3(256), 0, st, x, yd, wts, TK, H, ss);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
 int gemv_setup_lds() {
   int rc;
   if ((rc = setup_mt<1>()) || (rc = setup_mt<2>()) || (rc = setup_mt<3>()) || (rc = setup_mt<4>())) return rc;
+  const void* moe[] = {(const void*)moe_gemv_kernel<1>, (const void*)moe_gemv_kernel<2>, (const void*)moe_gemv_kernel<3>,
+                       (const void*)moe_gemv_kernel<4>, (const void*)moe_gemv_kernel<5>};
+  for (const void* f : moe)
+    MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)moe_lds_bytes(MOE_MAX_GP)));
   return MC_OK;
 }
 

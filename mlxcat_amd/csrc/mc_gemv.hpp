@@ -37,6 +37,46 @@ struct GemvArgs {
   unsigned long long* amax = nullptr;
 };
 
+// Grouped GEMV over the experts a verify block touches (Qwen3-MoE SwitchGLU).  Every
+// touched expert's tiles are streamed once for all the (token, slot) pairs routed to it.
+// Pairs are numbered t * TK + kk (token t, k-th selected expert); the routing kernel lists
+// them per touched expert in ascending order.
+struct MoeRoute {
+  int32_t* n_active = nullptr;  // [1] touched experts
+  int32_t* act_e = nullptr;     // [E] touched experts, ascending
+  int32_t* off = nullptr;       // [E + 1] offsets into pairs per touched expert
+  int32_t* pairs = nullptr;     // [M * TK] pair numbers grouped by expert
+  int32_t* sel = nullptr;       // [M * TK] selected expert of each pair
+  float* wts = nullptr;         // [M * TK] renormalised routing weight of each pair
+};
+
+struct MoeGemvArgs {
+  const uint32_t* qw = nullptr;  // expert 0 (tile layout); expert e at + e * qw_es words
+  const uint32_t* sb = nullptr;
+  size_t qw_es = 0, sb_es = 0;
+  int N = 0, K = 0, NT = 0, GP = 0;
+  const uint16_t* x = nullptr;   // input row of pair p: x + (p / x_div) * ldx
+  int ldx = 0, x_div = 1;
+  MoeRoute rt;
+  int epi = EPI_SWIGLU;          // EPI_SWIGLU: y[p][N / 2] bf16; EPI_STORE: yf[p][N] f32
+  uint16_t* y = nullptr;
+  float* yf = nullptr;
+  int ldy = 0;
+  int max_active = 0;            // touched experts, at most (grid rows)
+  int nb = 1;                    // blocks per touched expert
+  uint32_t dq_mask = DQ_MASK, dq_magic = DQ_MAGIC;
+};
+
+int moe_gemv_launch(const MoeGemvArgs& a, hipStream_t st);
+// xn[t] = RMSNorm(x[t]) * w for t < M (bf16 rows of width H)
+int launch_rows_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, float eps, uint16_t* xn, hipStream_t st);
+// softmax over the bf16 router logits, top-k (ties -> lower index), renormalised weights,
+// and the per-expert pair lists
+int launch_moe_route(const uint16_t* logits, int M, int E, int TK, const MoeRoute& rt, hipStream_t st);
+// x[t] = bf16(x[t] + sum_kk wts[t TK + kk] * yd[t TK + kk]) in kk order; ss[t * (H / 16) + j]
+// = sum of squares of the new row's 16-column tile j
+int launch_moe_combine(uint16_t* x, const float* yd, const float* wts, int M, int TK, int H, float* ss, hipStream_t st);
+
 size_t gemv_lds_bytes(int Mr, int kr, int MT);
 void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit);
 int gemv_launch(const GemvArgs& a, int MT, hipStream_t st);

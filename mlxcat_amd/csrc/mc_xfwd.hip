@@ -1177,6 +1177,7 @@ bool xfwd_supported(const mc_model_config& c, int R, int cap, int cus, const cha
   const char* r = nullptr;
   const int g = c.n_kv_heads > 0 ? c.n_q_heads / c.n_kv_heads : 0;
   if (cus % XF_XCD || cus < XF_XCD) r = "CU count is not a multiple of the XCD count";
+  else if (c.n_experts > 0) r = "mixture of experts";
   else if (c.n_kv_heads != XF_XCD) r = "kv heads != XCD count";
   else if (g != XF_G || g * c.n_kv_heads != c.n_q_heads) r = "GQA group != 4";
   else if (c.head_dim != 128) r = "head_dim != 128";

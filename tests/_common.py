@@ -6,7 +6,7 @@ import numpy as np
 # bf16 verify-logit tolerance (absolute, relative)
 ATOL, RTOL = 2e-2, 1e-2
 
-ARCH_QWEN3, ARCH_LLAMA = 0, 1
+ARCH_QWEN3, ARCH_LLAMA, ARCH_QWEN3_MOE = 0, 1, 2
 ARCH_FAKE_REPEATING, ARCH_FAKE_MISMATCHING = 100, 101
 
 
@@ -27,6 +27,16 @@ FAKE_MISMATCHING = cfg(ARCH_FAKE_MISMATCHING, 1, 64, 1, 1, 64, 64, 8, 1, 1e6)
 QWEN3_4B_2L = cfg(ARCH_QWEN3, 2, 2560, 32, 8, 128, 9728, 151936, 1, 1e6)
 # Llama-3-8B layer shapes with 1 layer
 LLAMA3_8B_1L = cfg(ARCH_LLAMA, 1, 4096, 32, 8, 128, 14336, 128256, 0, 5e5)
+
+
+def moe(base, n_experts, top_k, moe_inter):
+    return dict(base, n_experts=n_experts, n_experts_per_tok=top_k, moe_intermediate=moe_inter)
+
+
+# a small Qwen3-MoE decoder: 16 experts of width 128, top-4
+TINY_MOE = moe(cfg(ARCH_QWEN3_MOE, 2, 256, 4, 2, 64, 512, 4096, 1, 1e6), 16, 4, 128)
+# Qwen3-30B-A3B layer shapes with 1 layer: 128 experts of width 768, top-8, GQA group 8, untied head
+QWEN3_30B_A3B_1L = moe(cfg(ARCH_QWEN3_MOE, 1, 2048, 32, 4, 128, 6144, 151936, 0, 1e6), 128, 8, 768)
 
 
 def spec(enabled=True, k=4, max_suffix=16, min_ctx=8, acceptance=0, single_row_only=1, greedy_only=1):

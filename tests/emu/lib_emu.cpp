@@ -9,6 +9,7 @@
 //   case 2: Qwen3-4B shape (2 layers): 40-token prefill, a 6-token verify (persistent)
 //   case 3: case 0 with 32 q / 8 kv heads, hidden 512 (the XCD-partitioned forward; EMU_CUS=32)
 //   case 4: the case-3 model through mc_step (verify blocks with padding slots; MC_STEP_EAGER=1)
+//   case 5: a small Qwen3-MoE model (16 experts, top-4) through the multi-kernel forward
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -72,6 +73,9 @@ int main(int argc, char** argv) {
   if (cs == 4) {  // speculative steps through the XCD-partitioned forward: padding slots
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
+  if (cs == 5) {  // Qwen3-MoE: 16 experts of width 128, top-4 (a 40-token prefill gives experts > 16 pairs)
+    c.arch = MC_ARCH_QWEN3_MOE; c.n_experts = 16; c.n_experts_per_tok = 4; c.moe_intermediate = 128;
+  }
   const uint64_t SEED = 1234;
   const int ctx = 256, V = c.vocab;
   mc_model* m = nullptr;
@@ -116,7 +120,7 @@ int main(int argc, char** argv) {
     return g_bad ? 1 : 0;
   }
   or_config oc{c.arch, c.n_layers, c.hidden, c.n_q_heads, c.n_kv_heads, c.head_dim, c.intermediate, c.vocab,
-               c.tied_embeddings, c.rms_eps, c.rope_theta, 0, 0, 0};
+               c.tied_embeddings, c.rms_eps, c.rope_theta, c.n_experts, c.n_experts_per_tok, c.moe_intermediate};
   or_model* om = or_model_create(&oc, SEED, ctx, 1);
   uint64_t rng = 0x1234567ull;
   auto tokens = [&](int n) {
@@ -135,7 +139,7 @@ int main(int argc, char** argv) {
     or_forward(om, 1, &row0, &n, t.data(), nullptr);
     printf("prefill done\n");
   }
-  check(mc_batch_set_fused(b, cs == 1 ? 0 : 2), "set_fused");
+  check(mc_batch_set_fused(b, cs == 1 || cs == 5 ? 0 : 2), "set_fused");
   const std::vector<int> widths = cs == 2 ? std::vector<int>{6} : std::vector<int>{6, 1, 8};
   for (int w : widths) {
     auto t = tokens(w);

@@ -3,8 +3,8 @@ and the M-invariance the acceptance relies on (bit for bit)."""
 import numpy as np
 import pytest
 
-from tests._common import (LLAMA3_8B_1L, QWEN3_4B_2L, TINY, TINY_LLAMA, assert_close_bf16, assert_close_bf16_kv,
-                           assert_close_bf16_wide)
+from tests._common import (LLAMA3_8B_1L, QWEN3_30B_A3B_1L, QWEN3_4B_2L, TINY, TINY_LLAMA, TINY_MOE, assert_close_bf16,
+                           assert_close_bf16_kv, assert_close_bf16_wide, inside_fraction)
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -19,7 +19,7 @@ def pair(hip, oracle, cfg, rows=1, ctx=256, k=8):
     return gm, gb, om
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY_LLAMA], ids=["qwen3", "llama"])
+@pytest.mark.parametrize("cfg", [TINY, TINY_LLAMA, TINY_MOE], ids=["qwen3", "llama", "qwen3-moe"])
 def test_forward_matches_oracle(hip, oracle, cfg):
     gm, gb, om = pair(hip, oracle, cfg, rows=3)
     rng = np.random.default_rng(0)
@@ -55,6 +55,44 @@ def test_forward_full_shapes_match_oracle(hip, oracle, cfg):
         alt = om_rev.forward([0, 1], [6, 5], toks)
     assert_close_bf16_wide(gb.forward([0, 1], [6, 5], toks), om.forward([0, 1], [6, 5], toks), what="verify",
                            floor_u16=alt)
+
+
+def test_moe_full_shape_matches_oracle(hip, oracle):
+    """The Qwen3-30B-A3B-shape verify block of 4 rows x 5 tokens (M = 20): the grouped
+    expert GEMVs over 128 experts, top-8, and the GQA-8 attention, after uneven prefills."""
+    cfg = QWEN3_30B_A3B_1L
+    rows = 4
+    gm, gb, om = pair(hip, oracle, cfg, rows=rows, ctx=160)
+    om_rev = oracle.Model(cfg, SEED, 160, rows)
+    rng = np.random.default_rng(3)
+    V = cfg["vocab"]
+    lens = [30, 12, 17, 5]
+    toks = rng.integers(0, V, sum(lens)).tolist()
+    gb.forward(list(range(rows)), lens, toks, want_logits=False)
+    om.forward(list(range(rows)), lens, toks, want_logits=False)
+    with oracle.reversed_reduction_order():
+        om_rev.forward(list(range(rows)), lens, toks, want_logits=False)
+    toks = rng.integers(0, V, 5 * rows).tolist()
+    with oracle.reversed_reduction_order():
+        alt = om_rev.forward(list(range(rows)), [5] * rows, toks)
+    got = gb.forward(list(range(rows)), [5] * rows, toks)
+    want = om.forward(list(range(rows)), [5] * rows, toks)
+    # Routing near-ties: bf16 router logits of 128 experts often tie within an ulp at the
+    # top-8 boundary, so any change of summation order (the reordered oracle included)
+    # flips some token's expert set, and that token's logits diverge as a whole.  Tokens
+    # are classified by the fraction of their logits within the bound; the agreeing ones
+    # are held to the full-width criterion, the diverging ones counted against the
+    # reordered oracle's own count.
+    frac_got = [inside_fraction(got[t], want[t]) for t in range(len(toks))]
+    frac_alt = [inside_fraction(alt[t], want[t]) for t in range(len(toks))]
+    div_got = [t for t, f in enumerate(frac_got) if f < 0.99]
+    div_alt = [t for t, f in enumerate(frac_alt) if f < 0.99]
+    assert len(div_got) <= len(div_alt) + 3, (div_got, div_alt, [round(f, 3) for f in frac_got])
+    keep = [t for t in range(len(toks)) if t not in div_got and t not in div_alt]
+    assert len(keep) >= len(toks) // 2
+    assert_close_bf16_wide(got[keep], want[keep], what="moe verify (agreeing tokens)", floor_u16=alt[keep])
+    for r in range(rows):
+        assert gb.kv_len(r) == om.kv_len(r)
 
 
 def test_forward_long_context_split_kv(hip, oracle):

@@ -3,7 +3,7 @@ acceptance.  Integer and index results are compared bit for bit."""
 import numpy as np
 import pytest
 
-from tests._common import TINY, f32_to_bf16
+from tests._common import TINY, TINY_MOE, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -27,6 +27,29 @@ def test_synthetic_weights_match_oracle(hip, oracle):
             for g, w in zip(got, want):
                 np.testing.assert_array_equal(g, w, err_msg=f"layer {layer} slot {which}")
     for g, w in zip(gm.get_linear(-1, hip.W_EMBED), om.linear(-1, 0)):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_synthetic_expert_weights_match_oracle(hip, oracle):
+    """Qwen3-MoE: the router and every expert's gate / up / down, as the oracle generates them."""
+    gm = _model(hip, TINY_MOE)
+    om = oracle.Model(TINY_MOE, SEED, 16, 1)
+    for layer in range(TINY_MOE["n_layers"]):
+        for g, w in zip(gm.get_linear(layer, hip.W_ROUTER), om.linear(layer, 11)):
+            np.testing.assert_array_equal(g, w, err_msg=f"router {layer}")
+        for e in (0, 5, TINY_MOE["n_experts"] - 1):
+            for which in (hip.W_GATE, hip.W_UP, hip.W_DOWN):
+                for g, w in zip(gm.get_linear(layer, which, e), om.linear(layer, which, e)):
+                    np.testing.assert_array_equal(g, w, err_msg=f"layer {layer} expert {e} slot {which}")
+    rng = np.random.default_rng(6)
+    N, K = gm._lshape(hip.W_DOWN, 3)
+    wq = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint32)
+    sc = rng.integers(0, 2**16, (N, K // 64), dtype=np.uint16)
+    bi = rng.integers(0, 2**16, (N, K // 64), dtype=np.uint16)
+    gm.set_linear(1, hip.W_DOWN, wq, sc, bi, expert=3)
+    for g, w in zip(gm.get_linear(1, hip.W_DOWN, 3), (wq, sc, bi)):
+        np.testing.assert_array_equal(g, w)
+    for g, w in zip(gm.get_linear(1, hip.W_DOWN, 4), om.linear(1, 6, 4)):  # the neighbour is untouched
         np.testing.assert_array_equal(g, w)
 
 

@@ -6,13 +6,13 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from tests._common import TINY, TINY_LLAMA, assert_close_bf16, bf16_to_f32
+from tests._common import TINY, TINY_LLAMA, TINY_MOE, assert_close_bf16, bf16_to_f32
 
 SEED = 1234
 
 
-def dequant(O, m, layer, which):
-    wq, s, b = m.linear(layer, which)
+def dequant(O, m, layer, which, expert=-1):
+    wq, s, b = m.linear(layer, which, expert)
     N, KW = wq.shape
     q = np.zeros((N, KW * 8), dtype=np.float32)
     for j in range(8):
@@ -30,6 +30,24 @@ def norm_w(O, seed, tid, n):
     w = np.zeros(n, dtype=np.uint16)
     O.lib().or_gen_norm(seed, tid, n, w.ctypes.data_as(__import__("ctypes").c_void_p))
     return torch.from_numpy(bf16_to_f32(w))
+
+
+def torch_moe(O, m, cfg, l, h):
+    """Qwen3-MoE sparse block (Qwen3MoeSparseMoeBlock: router softmax in fp32, top-k,
+    norm_topk_prob renormalisation, SwiGLU experts) over the normalised rows h.  The router
+    logits are bf16 like every linear output of the model."""
+    E, TK = cfg["n_experts"], cfg["n_experts_per_tok"]
+    probs = torch.softmax(bf(h @ dequant(O, m, l, 11).T), dim=-1)
+    w, sel = torch.topk(probs, TK, dim=-1)
+    w = w / w.sum(dim=-1, keepdim=True)
+    out = torch.zeros_like(h)
+    for t in range(h.shape[0]):
+        for kk in range(TK):
+            e = int(sel[t, kk])
+            g = h[t] @ dequant(O, m, l, 4, e).T
+            u = h[t] @ dequant(O, m, l, 5, e).T
+            out[t] += w[t, kk] * (bf(F.silu(g) * u) @ dequant(O, m, l, 6, e).T)
+    return out
 
 
 def torch_forward(O, m, cfg, tokens, positions):
@@ -57,7 +75,7 @@ def torch_forward(O, m, cfg, tokens, positions):
         q = bf(h @ dequant(O, m, l, 0).T).view(T, nq, d)
         k = bf(h @ dequant(O, m, l, 1).T).view(T, nkv, d)
         v = bf(h @ dequant(O, m, l, 2).T).view(T, nkv, d)
-        if cfg["arch"] == 0:
+        if cfg["arch"] in (0, 2):
             q = bf(F.rms_norm(q, (d,), norm_w(O, SEED, tid(9), d), eps))
             k = bf(F.rms_norm(k, (d,), norm_w(O, SEED, tid(10), d), eps))
         q, k = rope(q), rope(k)
@@ -66,6 +84,9 @@ def torch_forward(O, m, cfg, tokens, positions):
         a = bf(a[0].transpose(0, 1).reshape(T, nq * d))
         x = bf(x + a @ dequant(O, m, l, 3).T)
         h = bf(F.rms_norm(x, (H,), norm_w(O, SEED, tid(8), H), eps))
+        if cfg["arch"] == 2:
+            x = bf(x + torch_moe(O, m, cfg, l, h))
+            continue
         g = h @ dequant(O, m, l, 4).T
         u = h @ dequant(O, m, l, 5).T
         x = bf(x + bf(F.silu(g) * u) @ dequant(O, m, l, 6).T)
@@ -74,7 +95,7 @@ def torch_forward(O, m, cfg, tokens, positions):
     return (h @ head.T).to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY_LLAMA], ids=["qwen3", "llama"])
+@pytest.mark.parametrize("cfg", [TINY, TINY_LLAMA, TINY_MOE], ids=["qwen3", "llama", "qwen3-moe"])
 def test_forward_vs_torch(oracle, cfg):
     m = oracle.Model(cfg, SEED, 64, 1)
     rng = np.random.default_rng(0)
