@@ -83,13 +83,14 @@ struct WBuf {
   uint2 sb[D];  // (scale | bias << 16) of this lane's weight row, groups 2gp and 2gp + 1
 };
 
-template <int D>
+// Pairs wave + WS i of the unit (WS = 1: all of them, for a wave that owns the unit).
+template <int D, int WS = GEMV_WAVES>
 __device__ inline void load_unit(WBuf<D>& w, const GemvArgs& a, int t, int gp0, int ngp, int wave, int lane, int r16) {
   const u32x4* qbase = reinterpret_cast<const u32x4*>(a.qw) + ((size_t)t * a.GP + gp0) * 64 + lane;
   const uint2* sbase = reinterpret_cast<const uint2*>(a.sb) + tile_sb_word(t, r16, gp0, 0, a.GP) / 2;
 #pragma unroll
   for (int i = 0; i < D; ++i) {
-    const int j = min(wave + GEMV_WAVES * i, ngp - 1);  // a short K-range re-reads its last pair
+    const int j = min(wave + WS * i, ngp - 1);  // a short K-range re-reads its last pair
     w.nib[i] = __builtin_nontemporal_load(qbase + (size_t)j * 64);
     w.sb[i] = sbase[j];
   }
@@ -99,14 +100,14 @@ __device__ inline void load_unit(WBuf<D>& w, const GemvArgs& a, int t, int gp0, 
 // operand (rows = tokens) and the weights its B operand (columns = weight rows), so lane
 // (c, r16) ends with tokens mt*16 + 4c + v (v = 0..3) of weight row 16t + r16 and applies
 // one row's scale and bias.  xsum is laid out [group][16 * MT tokens].
-template <int MT, int D>
+template <int MT, int D, int WS = GEMV_WAVES>
 __device__ inline void compute_unit(f32x4 (&acc)[MT], const WBuf<D>& w, const uint16_t* xl, const float* xsum, int XS,
                                     int Mr, int ngp, int wave, int c, int r16, uint32_t mask, uint32_t magic) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < D; ++i) {
-    const int j = wave + GEMV_WAVES * i;
+    const int j = wave + WS * i;
     if (j >= ngp) break;
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
@@ -446,19 +447,217 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// multi-row GEMV (16 < M <= 64): 8 waves per block, each wave owning whole units
+// ---------------------------------------------------------------------------------------
+// The activations of a K-range take Mr x kr x 256 bytes of LDS (up to 64 x 8 x 256), so
+// one or two blocks fit a CU; with 8 waves per block and a wave computing a unit's whole
+// K-range (no cross-wave reduction), every wave keeps the next unit's weights (up to 8
+// KiB) in flight while it computes the current one.
+constexpr int MID_WAVES = 8;
+constexpr int MID_THREADS = MID_WAVES * 64;
+constexpr int MID_KMAX = 8;  // the unit buffers of larger K-ranges are not kept in registers
+constexpr int MID_LDS_CAP = 150 * 1024;
+
+size_t mid_lds_bytes(int Mr, int kr, int MT) {
+  return (size_t)Mr * xrow_stride(kr) * 2 + (size_t)16 * MT * 2 * kr * 4 + 64 * 4 + (size_t)kr * 128 * 2;
+}
+
+template <int MT, int D>
+__global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
+  MC_DYN_LDS(smem);
+  const int kr_gp = a.kr, ks = a.ksplit;
+  const int XS = xrow_stride(kr_gp);
+  const int Mr = min(a.M, 16 * MT);
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                     // [Mr][XS]
+  float* xsum = reinterpret_cast<float*>(smem + (size_t)Mr * XS * 2);   // [2 kr][16 MT]
+  float* rs = xsum + 16 * MT * 2 * kr_gp;                               // [64] row scales
+  uint16_t* wl = reinterpret_cast<uint16_t*>(rs + 64);                  // [kr * 128] norm weights
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane >> 4, r16 = lane & 15;
+  const int kq = blockIdx.x % ks;
+  const int gp0 = kq * kr_gp, ngp = min(a.GP, gp0 + kr_gp) - gp0, k0 = gp0 * 128, ng = 2 * ngp;
+  const int tstride = (int)(gridDim.x / ks) * MID_WAVES;
+  const int t0 = (int)(blockIdx.x / ks) * MID_WAVES + wave;
+  const int cpr = ngp * 16, xtotal = Mr * cpr;
+  const unsigned cpr_magic = 0xFFFFFFFFu / (unsigned)cpr + 1u;
+
+  // ---- small loads first (vmcnt retires in order): norm partials, norm weights, the first
+  // pass of X; then the first unit's weights ----
+  constexpr int XCH = 4;
+  // norm partials: rows wave + 8 j (j < 8 covers Mr <= 64), producer tiles lane + 64 q (ss_nt <= 256)
+  float ssq[8][4];
+  if (a.norm_w) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = wave + MID_WAVES * j, tt = lane + 64 * q;
+        ssq[j][q] = (m < Mr && tt < a.ss_nt) ? a.ss_in[(size_t)m * a.ss_ld + tt] : 0.f;
+      }
+  }
+  u32x4 nw = {0u, 0u, 0u, 0u};
+  if (a.norm_w && tid < cpr && k0 + tid * 8 < a.K) nw = *reinterpret_cast<const u32x4*>(a.norm_w + k0 + tid * 8);
+  u32x4 xv[XCH];
+#pragma unroll
+  for (int q = 0; q < XCH; ++q) {
+    const int i = tid + MID_THREADS * q;
+    xv[q] = (u32x4){0u, 0u, 0u, 0u};
+    if (i < xtotal) {
+      const int m = (int)__umulhi((unsigned)i, cpr_magic), ch = i - m * cpr;
+      if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
+    }
+  }
+  WBuf<D> wa, wb;
+  load_unit<D, 1>(wa, a, min(t0, a.NT - 1), gp0, ngp, 0, lane, r16);
+
+  // ---- row scales of the fused RMSNorm, r[m] = 1 / sqrt(mean(x^2) + eps), fixed order ----
+  if (a.norm_w) {
+    if (tid < cpr) *reinterpret_cast<u32x4*>(wl + tid * 8) = nw;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float q = (ssq[j][0] + ssq[j][1]) + (ssq[j][2] + ssq[j][3]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+      const int m = wave + MID_WAVES * j;
+      if (lane == 0 && m < Mr) rs[m] = 1.0f / sqrtf(q / (float)a.K + a.eps);
+    }
+    lds_barrier();
+  }
+
+  // ---- X (normalised) into LDS with its group sums ----
+  for (int base = 0; base < xtotal; base += MID_THREADS * XCH) {
+    if (base > 0) {
+#pragma unroll
+      for (int q = 0; q < XCH; ++q) {
+        const int i = base + tid + MID_THREADS * q;
+        xv[q] = (u32x4){0u, 0u, 0u, 0u};
+        if (i < xtotal) {
+          const int m = (int)__umulhi((unsigned)i, cpr_magic), ch = i - m * cpr;
+          if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
+        }
+      }
+    }
+    int mm[XCH], cc[XCH];
+    bool in[XCH];
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int i = base + tid + MID_THREADS * q;
+      in[q] = i < xtotal;
+      mm[q] = (int)__umulhi((unsigned)i, cpr_magic);
+      cc[q] = i - mm[q] * cpr;
+    }
+    if (a.norm_w) {
+      float rr[XCH];
+      u32x4 ww[XCH];
+#pragma unroll
+      for (int q = 0; q < XCH; ++q) {
+        rr[q] = in[q] ? rs[mm[q]] : 0.f;
+        ww[q] = in[q] ? *reinterpret_cast<const u32x4*>(wl + cc[q] * 8) : (u32x4){0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int q = 0; q < XCH; ++q)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float lo = (__uint_as_float(xv[q][h] << 16) * rr[q]) * __uint_as_float(ww[q][h] << 16);
+          const float hi = (__uint_as_float(xv[q][h] & 0xFFFF0000u) * rr[q]) * __uint_as_float(ww[q][h] & 0xFFFF0000u);
+          xv[q][h] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+        }
+    }
+    float gs[XCH];
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      if (in[q]) *reinterpret_cast<u32x4*>(xl + mm[q] * XS + cc[q] * 8) = xv[q];
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        s0 += __uint_as_float(xv[q][h] << 16);
+        s1 += __uint_as_float(xv[q][h] & 0xFFFF0000u);
+      }
+      gs[q] = in[q] ? s0 + s1 : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) gs[q] = sum8_lanes(gs[q]);
+#pragma unroll
+    for (int q = 0; q < XCH; ++q)
+      if (in[q] && (cc[q] & 7) == 0) xsum[(cc[q] >> 3) * 16 * MT + mm[q]] = gs[q];
+  }
+  if (lane < 16 * MT - Mr)
+    for (int gl = wave; gl < ng; gl += MID_WAVES) xsum[gl * 16 * MT + Mr + lane] = 0.f;
+  lds_barrier();
+
+  // ---- units: the next one's weights in flight while this one is computed ----
+  const uint32_t mask = a.dq_mask;
+  uint32_t magic;
+  MC_TO_VGPR(magic, a.dq_magic);
+  const bool deferred = ks > 1 || a.epi == EPI_RESIDUAL;
+  int t = t0;
+  while (t < a.NT) {
+    {
+      const int tn = t + tstride < a.NT ? t + tstride : t;
+      load_unit<D, 1>(wb, a, tn, gp0, ngp, 0, lane, r16);
+      f32x4 acc[MT];
+      compute_unit<MT, D, 1>(acc, wa, xl, xsum, XS, Mr, ngp, 0, c, r16, mask, magic);
+      if (deferred) store_partial<MT>(a, acc, t, kq, lane);
+      else epilogue<MT>(a, acc, t, c, r16);
+      t += tstride;
+    }
+    if (t >= a.NT) break;
+    {
+      const int tn = t + tstride < a.NT ? t + tstride : t;
+      load_unit<D, 1>(wa, a, tn, gp0, ngp, 0, lane, r16);
+      f32x4 acc[MT];
+      compute_unit<MT, D, 1>(acc, wb, xl, xsum, XS, Mr, ngp, 0, c, r16, mask, magic);
+      if (deferred) store_partial<MT>(a, acc, t, kq, lane);
+      else epilogue<MT>(a, acc, t, c, r16);
+      t += tstride;
+    }
+  }
+  if (deferred) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int tt = t0; tt < a.NT; tt += tstride) arrive<MT>(a, tt, lane, c, r16);
+  }
+}
+
+// K-range plan of the multi-row classes: the largest K-range whose activations fit the LDS
+// cap (at most 8 group pairs), split further (down to 4 pairs) while the units cannot give
+// every wave of the device one.  Depends only on (N, K, MT) and the CU count.
+void mid_plan(const QLinear& L, int MT, int cus, int* kr, int* ksplit) {
+  int kmax = MID_KMAX;
+  while (kmax > 1 && mid_lds_bytes(16 * MT, kmax, MT) > (size_t)MID_LDS_CAP) --kmax;
+  int ks = (L.GP + kmax - 1) / kmax;
+  while ((size_t)L.NT * ks < (size_t)MID_WAVES * cus && (L.GP + ks) / (ks + 1) >= 4) ++ks;
+  *kr = (L.GP + ks - 1) / ks;
+  *ksplit = (L.GP + *kr - 1) / *kr;
+}
+
 // K-range plan of a shape for an M class (MT = 1: M <= 16; MT > 1: M <= 64).  Depends
 // only on (N, K, class): a token's reduction order never changes with the number of
 // tokens in its class, nor with the grid the launch gets.
+static int g_cus = 0;
+
+static int device_cus() {
+  if (g_cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus < 1)
+      g_cus = 1;
+  }
+  return g_cus;
+}
+
 void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit) {
-  const int Mr = MT == 1 ? 16 : 64;
+  if (MT > 1) {
+    mid_plan(L, MT, device_cus(), kr, ksplit);
+    return;
+  }
+  const int Mr = 16;
   // one K-range when it fits 5 group pairs per wave (no split-K tail), else 3 per wave
   int d = (MT == 1 && L.GP <= GEMV_WAVES * 5) ? 5 : 3;
   while (d > 1 && gemv_lds_bytes(Mr, GEMV_WAVES * d, MT) > (size_t)GEMV_LDS_LIMIT) --d;
   *kr = std::min(L.GP, GEMV_WAVES * d);
   *ksplit = (L.GP + *kr - 1) / *kr;
 }
-
-static int g_cus = 0;
 
 // resident blocks per CU of one kernel instance at one LDS size (cached)
 template <int MT, int D, int U>
@@ -504,33 +703,41 @@ static void launch_md(const GemvArgs& a, size_t lds, hipStream_t st) {
 
 template <int MT>
 static void launch_mt(const GemvArgs& a, int D, size_t lds, hipStream_t st) {
-  if constexpr (MT > 1) {  // the large-M classes use at most 2 group pairs per wave (LDS)
-    if (D <= 1) launch_md<MT, 1>(a, lds, st);
-    else launch_md<MT, 2>(a, lds, st);
-  } else {
-    switch (D) {
-      case 1: launch_md<MT, 1>(a, lds, st); break;
-      case 2: launch_md<MT, 2>(a, lds, st); break;
-      case 3: launch_md<MT, 3>(a, lds, st); break;
-      case 4: launch_md<MT, 4>(a, lds, st); break;
-      default: launch_md<MT, 5>(a, lds, st); break;
-    }
+  switch (D) {
+    case 1: launch_md<MT, 1>(a, lds, st); break;
+    case 2: launch_md<MT, 2>(a, lds, st); break;
+    case 3: launch_md<MT, 3>(a, lds, st); break;
+    case 4: launch_md<MT, 4>(a, lds, st); break;
+    default: launch_md<MT, 5>(a, lds, st); break;
   }
 }
 
+template <int MT, int D>
+static void launch_mid_d(const GemvArgs& a, size_t lds, hipStream_t st) {
+  int occ = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qgemv_mid_kernel<MT, D>, MID_THREADS, lds) !=
+          hipSuccess || occ < 1)
+    occ = 1;
+  const int groups = (a.NT + MID_WAVES - 1) / MID_WAVES;
+  const int G1 = std::max(1, std::min(groups, device_cus() * occ / a.ksplit));
+  hipLaunchKernelGGL((qgemv_mid_kernel<MT, D>), dim3(G1 * a.ksplit), dim3(MID_THREADS), lds, st, a);
+}
+
+template <int MT>
+static void launch_mid(const GemvArgs& a, size_t lds, hipStream_t st) {
+  if (a.kr <= 4) launch_mid_d<MT, 4>(a, lds, st);
+  else if (a.kr <= 6) launch_mid_d<MT, 6>(a, lds, st);
+  else launch_mid_d<MT, 8>(a, lds, st);
+}
+
 int gemv_launch(const GemvArgs& a, int MT, hipStream_t st) {
-  if (g_cus == 0) {
-    int dev = 0;
-    MC_HIP(hipGetDevice(&dev));
-    MC_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (g_cus < 1) g_cus = 1;
-  }
+  (void)device_cus();
   const int Mr = std::min(a.M, 16 * MT);
-  const size_t lds = gemv_lds_bytes(Mr, a.kr, MT);
+  const size_t lds = MT > 1 ? mid_lds_bytes(Mr, a.kr, MT) : gemv_lds_bytes(Mr, a.kr, MT);
   if (lds > (size_t)GEMV_LDS_LIMIT) return fail(MC_E_INVALID, "gemv: K-range exceeds LDS");
   if (a.M < 1 || a.M > 16 * MT || (MT > 1 && a.M <= 16)) return fail(MC_E_INVALID, "gemv: M outside the m-tile class");
   if (a.K % 64 || a.GP != (a.K + 127) / 128 || a.NT != (a.N + 15) / 16) return fail(MC_E_INVALID, "gemv: bad shape");
-  if (a.kr < 1 || a.kr > GEMV_WAVES * 5 || a.ksplit != (a.GP + a.kr - 1) / a.kr)
+  if (a.kr < 1 || a.kr > (MT > 1 ? MID_KMAX : GEMV_WAVES * 5) || a.ksplit != (a.GP + a.kr - 1) / a.kr)
     return fail(MC_E_INVALID, "gemv: bad K-range plan");
   if (a.norm_w && (!a.ss_in || a.ss_nt < 1 || a.ss_nt > 256 || a.ss_ld < a.ss_nt))
     return fail(MC_E_INVALID, "gemv: fused norm needs the producer's sums of squares (<= 256 tiles)");
@@ -543,9 +750,9 @@ int gemv_launch(const GemvArgs& a, int MT, hipStream_t st) {
   const int D = (a.kr + GEMV_WAVES - 1) / GEMV_WAVES;  // group pairs per wave per unit
   switch (MT) {
     case 1: launch_mt<1>(a, D, lds, st); break;
-    case 2: launch_mt<2>(a, D, lds, st); break;
-    case 3: launch_mt<3>(a, D, lds, st); break;
-    case 4: launch_mt<4>(a, D, lds, st); break;
+    case 2: launch_mid<2>(a, lds, st); break;
+    case 3: launch_mid<3>(a, lds, st); break;
+    case 4: launch_mid<4>(a, lds, st); break;
     default: return fail(MC_E_INVALID, "gemv: unsupported m-tile count");
   }
   MC_HIP(hipGetLastError());
@@ -736,11 +943,14 @@ int launch_rows_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, floa
 
 // One block.  Wave w routes tokens w, w + 4, ...: the E <= 256 bf16 logits (4 per lane),
 // softmax in fp32, TK rounds of the largest remaining probability (lowest expert on
-// ties), weights renormalised over the selection in selection order.  Then thread e
-// counts expert e's pairs, thread 0 forms the touched-expert list and offsets, and
-// thread e writes its pairs in ascending order.
+// ties), weights renormalised over the selection in selection order.  The selections stay
+// in LDS: thread e counts expert e's pairs, a scan over the experts gives the touched
+// list and the offsets, and thread e writes its pairs in ascending order.
+constexpr int MOE_ROUTE_PAIRS = 64 * 8;  // M <= 64 tokens x TK <= 8
+
 __global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, int M, int E, int TK, MoeRoute rt) {
-  __shared__ int cnt[256], slot_of[256];
+  __shared__ int s_sel[MOE_ROUTE_PAIRS];
+  __shared__ int s_cnt[256], s_act[256], s_cum[256];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int t = wave; t < M; t += 4) {
     float p[4];
@@ -764,8 +974,7 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] /= den;
     unsigned taken = 0u;  // bit j: expert lane + 64 j already selected
-    float wsel[8], wsum = 0.f;
-    int esel[8];
+    float wsum = 0.f, wmine = 0.f;
     for (int kk = 0; kk < TK; ++kk) {
       // key: probability bits (non-negative floats order as unsigned) over the inverted index
       unsigned long long best = 0ull;
@@ -783,50 +992,52 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, 
         best = ot > best ? ot : best;
       }
       const int ex = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
+      const float w = __uint_as_float((unsigned)(best >> 32));
       if ((ex & 63) == lane) taken |= 1u << (ex >> 6);
-      esel[kk] = ex;
-      wsel[kk] = __uint_as_float((unsigned)(best >> 32));
-      wsum += wsel[kk];
+      wsum += w;
+      if (lane == kk) wmine = w;  // lane kk keeps the kk-th selection's weight
+      if (lane == 0) s_sel[t * TK + kk] = ex;
     }
-    if (lane == 0)
-      for (int kk = 0; kk < TK; ++kk) {
-        rt.sel[t * TK + kk] = esel[kk];
-        rt.wts[t * TK + kk] = wsel[kk] / wsum;
-      }
+    if (lane < TK) {
+      rt.wts[t * TK + lane] = wmine / wsum;
+    }
   }
   __syncthreads();
   const int P = M * TK;
-  if (tid < E) {
-    int n = 0;
-    for (int i = 0; i < P; ++i) n += rt.sel[i] == tid;
-    cnt[tid] = n;
-  }
+  for (int i = tid; i < P; i += 256) rt.sel[i] = s_sel[i];
+  int n = 0;
+  if (tid < E)
+    for (int i = 0; i < P; ++i) n += s_sel[i] == tid;
+  s_cnt[tid] = n;
+  s_act[tid] = n > 0 ? 1 : 0;
   __syncthreads();
-  if (tid == 0) {
-    int na = 0, o = 0;
-    for (int ex = 0; ex < E; ++ex) {
-      slot_of[ex] = -1;
-      if (cnt[ex] == 0) continue;
-      slot_of[ex] = na;
-      rt.act_e[na] = ex;
-      rt.off[na] = o;
-      o += cnt[ex];
-      ++na;
-    }
-    rt.off[na] = o;
-    *rt.n_active = na;
+  // inclusive scans of the pair counts and of the touched flags (Hillis-Steele)
+  for (int o = 1; o < 256; o <<= 1) {
+    const int c0 = tid >= o ? s_cnt[tid - o] : 0, a0 = tid >= o ? s_act[tid - o] : 0;
+    __syncthreads();
+    s_cnt[tid] += c0;
+    s_act[tid] += a0;
+    __syncthreads();
   }
-  __syncthreads();
-  if (tid < E && slot_of[tid] >= 0) {
-    int o = rt.off[slot_of[tid]];
+  const int first = s_cnt[tid] - n;  // exclusive offset of expert tid's pairs
+  if (n > 0) {
+    const int slot = s_act[tid] - 1;
+    rt.act_e[slot] = tid;
+    rt.off[slot] = first;
+    int o = first;
     for (int i = 0; i < P; ++i)
-      if (rt.sel[i] == tid) rt.pairs[o++] = i;
+      if (s_sel[i] == tid) rt.pairs[o++] = i;
+  }
+  if (tid == 255) {
+    rt.off[s_act[255]] = s_cnt[255];
+    *rt.n_active = s_act[255];
   }
 }
 
 int launch_moe_route(const uint16_t* logits, int M, int E, int TK, const MoeRoute& rt, hipStream_t st) {
   if (E < 1 || E > 256 || TK < 1 || TK > 8 || TK > E) return fail(MC_E_INVALID, "moe route: experts (<= 256) / top-k (<= 8)");
   if (M < 1) return MC_OK;
+  if (M * TK > MOE_ROUTE_PAIRS) return fail(MC_E_INVALID, "moe route: more than 64 tokens");
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, st, logits, M, E, TK, rt);
   MC_HIP(hipGetLastError());
   return MC_OK;
@@ -862,7 +1073,13 @@ int launch_moe_combine(uint16_t* x, const float* yd, const float* wts, int M, in
 
 int gemv_setup_lds() {
   int rc;
-  if ((rc = setup_mt<1>()) || (rc = setup_mt<2>()) || (rc = setup_mt<3>()) || (rc = setup_mt<4>())) return rc;
+  if ((rc = setup_mt<1>())) return rc;
+  const void* mid[] = {(const void*)qgemv_mid_kernel<2, 4>, (const void*)qgemv_mid_kernel<2, 6>,
+                       (const void*)qgemv_mid_kernel<2, 8>, (const void*)qgemv_mid_kernel<3, 4>,
+                       (const void*)qgemv_mid_kernel<3, 6>, (const void*)qgemv_mid_kernel<3, 8>,
+                       (const void*)qgemv_mid_kernel<4, 4>, (const void*)qgemv_mid_kernel<4, 6>,
+                       (const void*)qgemv_mid_kernel<4, 8>};
+  for (const void* f : mid) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, MID_LDS_CAP));
   const void* moe[] = {(const void*)moe_gemv_kernel<1>, (const void*)moe_gemv_kernel<2>, (const void*)moe_gemv_kernel<3>,
                        (const void*)moe_gemv_kernel<4>, (const void*)moe_gemv_kernel<5>};
   for (const void* f : moe)
