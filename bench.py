@@ -9,9 +9,10 @@ positions copied from earlier spans.  A step is one speculative step (n-gram pro
 the timed region.  The same workload at batch 8 is reported beside it.
 
 Prints one JSON line: accepted tokens/s at batch 1 (value), the batch-8 figure, the
-verify-step latency, the live HBM roofline of the dominant kernel (the persistent forward
-kernel when the step runs it, else the dequant GEMV; timed with HIP events on its stream)
-and the CPU oracle timed on a bounded sample.
+verify-step latency, the live HBM roofline of the dominant kernel (the dequant GEMV, or
+the persistent forward kernel when the step runs it; timed with HIP events on its stream),
+its measured HBM traffic per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, recorded in
+profiles/), and the CPU oracle timed on a bounded sample.
 """
 from __future__ import annotations
 
@@ -31,6 +32,19 @@ QWEN3_4B = dict(arch=0, n_layers=36, hidden=2560, n_q_heads=32, n_kv_heads=8, he
                 vocab=151936, tied_embeddings=1, rms_eps=1e-6, rope_theta=1e6, n_experts=0, n_experts_per_tok=0,
                 moe_intermediate=0)
 K_DRAFT, MATCH, PROMPT_LEN, SEED = 5, 3, 2048, 1234
+# HBM bytes per launch of the verify GEMVs, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+# (scaled by the same counters over a plain 256 MiB copy); the commands are in the
+# summary beside this file
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_traffic_qwen3_4b_k5.json")
+
+
+def measured_traffic(kernel: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t.get("traffic_bytes_per_launch") if t.get("kernel") == kernel else None
 
 
 def spec_cfg(rows: int) -> dict:
@@ -134,10 +148,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
-    ap.add_argument("--forward", choices=["auto", "fused", "multi"], default="auto",
-                    help="verify forward: persistent kernel when possible (auto), required, or never")
+    ap.add_argument("--forward", choices=["multi", "persistent", "auto"], default="multi",
+                    help="verify forward: the per-layer kernels (the faster path on MI355X today), the persistent "
+                         "forward kernel (required), or the persistent kernel whenever the shape allows it")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="only copy 256 MiB three times (a plain copy kernel of known size: the scale of the "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
-    mode = {"auto": 1, "fused": 2, "multi": 0}[a.forward]
+    if a.copy_ref:
+        import torch
+        src = torch.ones(256 << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("copied 3 x 256 MiB", flush=True)
+        return
+    mode = {"auto": 1, "persistent": 2, "multi": 0}[a.forward]
     if a.gpus != 1:
         print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -171,7 +198,7 @@ def main():
                             "frac": round(b1["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
                             "bytes_per_step": b1["bytes_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(g["kernel"]),
                      "kernel": g["kernel"], "launches_per_step": g["launches"],
                      "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 3),
                      "alg_bytes_per_launch": round(g["bytes"] / max(1, g["launches"]))},
