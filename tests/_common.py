@@ -33,6 +33,8 @@ def moe(base, n_experts, top_k, moe_inter):
     return dict(base, n_experts=n_experts, n_experts_per_tok=top_k, moe_intermediate=moe_inter)
 
 
+# Qwen3-8B layer shapes with 1 layer and a 4096-token vocab (the M = 288 verify of 32 rows x 9)
+QWEN3_8B_1L_V4K = cfg(ARCH_QWEN3, 1, 4096, 32, 8, 128, 12288, 4096, 0, 1e6)
 # a small Qwen3-MoE decoder: 16 experts of width 128, top-4
 TINY_MOE = moe(cfg(ARCH_QWEN3_MOE, 2, 256, 4, 2, 64, 512, 4096, 1, 1e6), 16, 4, 128)
 # Qwen3-30B-A3B layer shapes with 1 layer: 128 experts of width 768, top-8, GQA group 8, untied head

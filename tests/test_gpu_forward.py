@@ -3,7 +3,8 @@ and the M-invariance the acceptance relies on (bit for bit)."""
 import numpy as np
 import pytest
 
-from tests._common import (LLAMA3_8B_1L, QWEN3_30B_A3B_1L, QWEN3_4B_2L, TINY, TINY_LLAMA, TINY_MOE, assert_close_bf16,
+from tests._common import (LLAMA3_8B_1L, QWEN3_30B_A3B_1L, QWEN3_4B_2L, QWEN3_8B_1L_V4K, TINY, TINY_LLAMA, TINY_MOE,
+                           assert_close_bf16,
                            assert_close_bf16_kv, assert_close_bf16_wide, inside_fraction)
 
 pytestmark = pytest.mark.gpu
@@ -55,6 +56,52 @@ def test_forward_full_shapes_match_oracle(hip, oracle, cfg):
         alt = om_rev.forward([0, 1], [6, 5], toks)
     assert_close_bf16_wide(gb.forward([0, 1], [6, 5], toks), om.forward([0, 1], [6, 5], toks), what="verify",
                            floor_u16=alt)
+
+
+def _rows_block_vs_oracle(hip, oracle, cfg, rows, ctx, prefill, width, seed):
+    """Uneven prefills of `rows` rows, then one verify block of `width` tokens per row,
+    against the oracle with the reordered-oracle floor."""
+    gm, gb, om = pair(hip, oracle, cfg, rows=rows, ctx=ctx, k=width - 1)
+    om_rev = oracle.Model(cfg, SEED, ctx, rows)
+    rng = np.random.default_rng(seed)
+    V = cfg["vocab"]
+    lens = [int(x) for x in rng.integers(prefill // 2, prefill + 1, rows)]
+    toks = rng.integers(0, V, sum(lens)).tolist()
+    # prefill in calls of at most 64 tokens
+    done = [0] * rows
+    while any(d < n for d, n in zip(done, lens)):
+        rs, cs, ts, budget = [], [], [], 64
+        for r in range(rows):
+            k = min(lens[r] - done[r], budget)
+            if k > 0:
+                off = sum(lens[:r]) + done[r]
+                rs.append(r); cs.append(k); ts += toks[off:off + k]
+                done[r] += k
+                budget -= k
+            if budget == 0:
+                break
+        gb.forward(rs, cs, ts, want_logits=False)
+        om.forward(rs, cs, ts, want_logits=False)
+        with oracle.reversed_reduction_order():
+            om_rev.forward(rs, cs, ts, want_logits=False)
+    vt = rng.integers(0, V, width * rows).tolist()
+    with oracle.reversed_reduction_order():
+        alt = om_rev.forward(list(range(rows)), [width] * rows, vt)
+    assert_close_bf16_wide(gb.forward(list(range(rows)), [width] * rows, vt), om.forward(list(range(rows)), [width] * rows, vt),
+                           what=f"verify of {rows} x {width}", floor_u16=alt)
+    for r in range(rows):
+        assert gb.kv_len(r) == om.kv_len(r)
+
+
+def test_batch8_llama3_8b_shape_matches_oracle(hip, oracle):
+    """8 rows x K+1 = 5 tokens (M = 40): the multi-row GEMV at the Llama-3-8B shapes."""
+    _rows_block_vs_oracle(hip, oracle, LLAMA3_8B_1L, rows=8, ctx=96, prefill=40, width=5, seed=4)
+
+
+def test_m288_qwen3_8b_shape_matches_oracle(hip, oracle):
+    """32 rows x K+1 = 9 tokens (M = 288, five launches of at most 64 rows) at the Qwen3-8B
+    layer shapes."""
+    _rows_block_vs_oracle(hip, oracle, QWEN3_8B_1L_V4K, rows=32, ctx=48, prefill=16, width=9, seed=5)
 
 
 def test_moe_full_shape_matches_oracle(hip, oracle):
