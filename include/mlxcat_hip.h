@@ -75,7 +75,9 @@ typedef struct mc_model mc_model;
 typedef struct mc_batch mc_batch;
 
 /* Model shape.  Mirrors the config.json keys an MLX checkpoint carries
- * (Sources/MLXCatNative/NativeModelEngine.swift:1147-1231). */
+ * (Sources/MLXCatNative/NativeModelEngine.swift:1147-1231).  Supported: head_dim 64 or 128,
+ * hidden a multiple of 64 up to 4096; Qwen3-MoE up to 256 experts, top-k <= 8, hidden and
+ * moe_intermediate up to 2560. */
 typedef struct mc_model_config {
   int32_t arch;
   int32_t n_layers, hidden, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;

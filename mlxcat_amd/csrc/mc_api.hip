@@ -149,7 +149,7 @@ extern "C" int mc_model_create(const mc_model_config* cfg, mc_model** out) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: architecture not supported by this build");
   }
-  if (c.n_layers <= 0 || c.hidden % 64 || c.hidden > 4096 || c.head_dim > 128 || c.head_dim % 16 || c.n_kv_heads <= 0 ||
+  if (c.n_layers <= 0 || c.hidden % 64 || c.hidden > 4096 || (c.head_dim != 64 && c.head_dim != 128) || c.n_kv_heads <= 0 ||
       c.n_q_heads % c.n_kv_heads || c.intermediate % 64 || c.vocab <= 0 || (c.n_q_heads * c.head_dim) % 64) {
     delete m;
     return fail(MC_E_INVALID, "mc_model_create: unsupported shape");

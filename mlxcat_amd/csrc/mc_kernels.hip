@@ -149,234 +149,6 @@ int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uin
 }
 
 // ---------------------------------------------------------------------------
-// split-KV attention on the matrix cores.  Grid (R * nkv, nchunk); block 256 = 4 waves.
-// A block stages one 64-key chunk of one (row, kv head) in LDS once -- K as [key][d],
-// V transposed to [d][key] -- and every query of the row that shares the kv head (the
-// verify positions x the GQA group) is scored against it: wave w takes query tiles
-// w, w + 4, ... of 16 queries.  Per tile:
-//   S = Q K^T   4 key blocks x 4 d-steps of v_mfma_f32_16x16x32_bf16,
-//   causal mask by absolute position, row max / sum over the chunk,
-//   O = P V     8 d blocks x 2 key-steps, P split into bf16 hi + lo parts,
-// and the partial (max, sum, O[d]) is written for the combine pass, which merges the
-// chunks in order: a query's result depends only on its own position and keys.
-// ---------------------------------------------------------------------------
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
-
-constexpr int KS_STRIDE = 128 + 8;        // LDS row stride (bf16) of K [key][d]
-constexpr int VT_STRIDE = ATTN_CHUNK + 8; // LDS row stride (bf16) of V^T [d][key]
-constexpr int PL_STRIDE = ATTN_CHUNK + 8; // LDS row stride (bf16) of P [q][key] (hi and lo parts)
-
-__global__ void __launch_bounds__(256) attn_partial_kernel(const uint16_t* q, KVLayer kv, SlotView sv, int nq,
-                                                           int nkv, int d, float scale, AttnWork w) {
-  __shared__ __align__(16) uint16_t ks[ATTN_CHUNK * KS_STRIDE];
-  __shared__ __align__(16) uint16_t vt[128 * VT_STRIDE];
-  __shared__ __align__(16) uint16_t pl[4 * 2 * 16 * PL_STRIDE];
-
-  const int G = nq / nkv;
-  const int r = blockIdx.x / nkv, kh = blockIdx.x % nkv;
-  const int chunk = blockIdx.y;
-  const int nv = sv.n_valid[r];
-  const int nqry = nv * G;
-  if (nqry == 0) return;
-  const int base = sv.qbase[r];
-  const int kend = base + nv;  // keys visible to the last query
-  const int k0 = chunk * ATTN_CHUNK;
-  if (k0 >= kend) return;
-  const int nk = min(ATTN_CHUNK, kend - k0);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int c = lane >> 4, r16 = lane & 15;
-  const int slot0 = sv.row_slot0[r];
-  typedef unsigned u4 __attribute__((ext_vector_type(4)));
-
-  // ---- stage the chunk: 16-byte loads of K [key][d] and of V^T [d][key] (the cache
-  // layout); keys >= nk are zero ----
-  const uint16_t* kbase = kv.k + (((size_t)r * nkv + kh) * kv.cap + k0) * d;
-  const uint16_t* vbase = kv.v + ((size_t)r * nkv + kh) * d * kv.cap + k0;
-  const int cpk = d / 8;  // 16-byte chunks per key row
-  for (int i = tid; i < ATTN_CHUNK * cpk; i += 256) {
-    const int key = i / cpk, e = (i - key * cpk) * 8;
-    u4 kk = {0u, 0u, 0u, 0u};
-    if (key < nk) kk = *reinterpret_cast<const u4*>(kbase + (size_t)key * d + e);
-    *reinterpret_cast<u4*>(ks + key * KS_STRIDE + e) = kk;
-  }
-  for (int i = tid; i < d * (ATTN_CHUNK / 8); i += 256) {
-    const int e = i / (ATTN_CHUNK / 8), kc = (i % (ATTN_CHUNK / 8)) * 8;
-    u4 vv = {0u, 0u, 0u, 0u};
-    if (kc < nk) {
-      vv = *reinterpret_cast<const u4*>(vbase + (size_t)e * kv.cap + kc);
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {  // zero the keys >= nk
-        if (kc + 2 * h >= nk) vv[h] &= 0xFFFF0000u;
-        if (kc + 2 * h + 1 >= nk) vv[h] &= 0x0000FFFFu;
-      }
-    }
-    *reinterpret_cast<u4*>(vt + e * VT_STRIDE + kc) = vv;
-  }
-  // d < 128: zero the unused d rows of V^T and d columns of K so the MFMA steps see zeros
-  for (int i = tid; i < (128 - d) * ATTN_CHUNK; i += 256) {
-    const int e = d + i / ATTN_CHUNK, key = i % ATTN_CHUNK;
-    vt[e * VT_STRIDE + key] = 0;
-    ks[key * KS_STRIDE + e] = 0;
-  }
-  __syncthreads();
-
-  const int nqt = (nqry + 15) / 16;
-  uint16_t* pw = pl + wave * 2 * 16 * PL_STRIDE;  // [hi | lo][16][PL_STRIDE]
-  const bf16x8_t zero8 = __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
-  for (int qt = wave; qt < nqt; qt += 4) {
-    // A operand: query qt*16 + r16, d = 32s + 8c .. +7
-    const int qa = qt * 16 + r16;
-    bf16x8_t qa_v[4];
-    if (qa < nqry) {
-      const int j = qa / G, gh = qa - j * G;
-      const uint16_t* qp = q + (size_t)(slot0 + j) * nq * d + (size_t)(kh * G + gh) * d;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        qa_v[s4] = (32 * s4 + 8 * c < d) ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * s4 + 8 * c) : zero8;
-    } else {
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) qa_v[s4] = zero8;
-    }
-    // S[q = 4c + v][key = 16 kb + r16]
-    f32x4_t sc[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const bf16x8_t kb_v = *reinterpret_cast<const bf16x8_t*>(ks + (kb * 16 + r16) * KS_STRIDE + 32 * s4 + 8 * c);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_v[s4], kb_v, acc, 0, 0, 0);
-      }
-      sc[kb] = acc;
-    }
-    // mask, row max / sum over the chunk (rows 4c + v live in the 16 lanes of group c)
-    float mx[4], lsum[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int qi = qt * 16 + 4 * c + v;
-      const int qpos = qi < nqry ? base + qi / G : -1;
-      float m = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const int key = kb * 16 + r16;
-        const bool ok = key < nk && k0 + key <= qpos;
-        const float s = ok ? sc[kb][v] * scale : -INFINITY;
-        sc[kb][v] = s;
-        m = fmaxf(m, s);
-      }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-      float l = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        // p = hi + lo exactly to ~2^-16: two bf16 MFMA operands keep P V near fp32
-        const float p = (sc[kb][v] == -INFINITY) ? 0.f : __expf(sc[kb][v] - m);
-        const uint16_t ph = f32_to_bf16(p);
-        const uint16_t plo = f32_to_bf16(p - bf16_to_f32(ph));
-        pw[(4 * c + v) * PL_STRIDE + kb * 16 + r16] = ph;
-        pw[(16 + 4 * c + v) * PL_STRIDE + kb * 16 + r16] = plo;
-        l += p;
-      }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
-      mx[v] = m;
-      lsum[v] = l;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's P writes are in LDS
-    __builtin_amdgcn_wave_barrier();
-    // O[q = 4c + v][d = 16 db + r16] = sum_key P[q][key] V[key][d]
-    bf16x8_t pa[2], pb2[2];
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      pa[k2] = *reinterpret_cast<const bf16x8_t*>(pw + r16 * PL_STRIDE + 32 * k2 + 8 * c);
-      pb2[k2] = *reinterpret_cast<const bf16x8_t*>(pw + (16 + r16) * PL_STRIDE + 32 * k2 + 8 * c);
-    }
-    const int nd16 = d / 16;
-    for (int db = 0; db < nd16; ++db) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const bf16x8_t vb = *reinterpret_cast<const bf16x8_t*>(vt + (db * 16 + r16) * VT_STRIDE + 32 * k2 + 8 * c);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[k2], vb, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb2[k2], vb, acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int qi = qt * 16 + 4 * c + v;
-        if (qi >= nqry) continue;
-        const int j = qi / G, gh = qi - j * G;
-        const int slot = slot0 + j, h = kh * G + gh;
-        w.part_o[(((size_t)slot * nq + h) * w.nchunk + chunk) * d + db * 16 + r16] = acc[v];
-      }
-    }
-    if (r16 == 0) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int qi = qt * 16 + 4 * c + v;
-        if (qi >= nqry) continue;
-        const int j = qi / G, gh = qi - j * G;
-        const int slot = slot0 + j, h = kh * G + gh;
-        float* pml = w.part_ml + (((size_t)slot * nq + h) * w.nchunk + chunk) * 2;
-        pml[0] = mx[v];
-        pml[1] = lsum[v];
-      }
-    }
-    __builtin_amdgcn_wave_barrier();  // P of this tile is consumed before the next tile overwrites it
-  }
-}
-
-// One wave per (slot, head): merge the chunk partials 0..nc-1 in chunk order with a running
-// max (each lane owns d/64 output elements); loads of 8 chunks are in flight at a time.
-__global__ void __launch_bounds__(256) attn_combine_kernel(SlotView sv, int M, int nq, int d, AttnWork w, uint16_t* att) {
-  const int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
-  if (wid >= M * nq) return;
-  const int m = wid / nq, h = wid - m * nq;
-  uint16_t* out = att + ((size_t)m * nq + h) * d;
-  const int row = sv.slot_row[m];
-  const int e0 = lane * 2;  // d <= 128: lane owns elements e0, e0 + 1
-  if (row < 0) {
-    if (e0 < d) *reinterpret_cast<uint32_t*>(out + e0) = 0u;
-    return;
-  }
-  const int pos = sv.slot_pos[m];
-  const int nc = pos / ATTN_CHUNK + 1;
-  const float* pml = w.part_ml + ((size_t)m * nq + h) * w.nchunk * 2;
-  const float* po = w.part_o + ((size_t)m * nq + h) * w.nchunk * d;
-  float mx = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
-  constexpr int UN = 8;
-  for (int c0 = 0; c0 < nc; c0 += UN) {
-    float2 ml[UN], ov[UN];
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int c = c0 + u;
-      ml[u] = make_float2(-INFINITY, 0.f);
-      ov[u] = make_float2(0.f, 0.f);
-      if (c < nc) {
-        ml[u] = *reinterpret_cast<const float2*>(pml + (size_t)c * 2);
-        if (e0 < d) ov[u] = *reinterpret_cast<const float2*>(po + (size_t)c * d + e0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const float cm = ml[u].x;
-      if (cm == -INFINITY) continue;  // a chunk with no visible key
-      const float nm = fmaxf(mx, cm);
-      const float fo = (mx == -INFINITY) ? 0.f : __expf(mx - nm);
-      const float fn = __expf(cm - nm);
-      l = l * fo + ml[u].y * fn;
-      a0 = a0 * fo + ov[u].x * fn;
-      a1 = a1 * fo + ov[u].y * fn;
-      mx = nm;
-    }
-  }
-  if (e0 < d) {
-    const float inv = 1.0f / l;
-    *reinterpret_cast<uint32_t*>(out + e0) = (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Split-KV attention, flash-decoding style, without LDS staging of K/V.  Grid
 // (R * nkv, splits); block (row, kv head, split) covers keys [split S 64, (split+1) S 64)
 // of the row, wave w its 64-key sub-chunks w, w + 4, ... (S >= 4).  K rows and V^T rows
@@ -390,6 +162,8 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(SlotView sv, int M, i
 // merged through LDS in wave order into one partial per (query, split); a query's result
 // depends only on its own position and keys.
 // ---------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 constexpr int FA_TP = 2;  // query tiles of 16 per pass
 
@@ -615,24 +389,17 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(SlotView sv, int M, int
 
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
                      int M, const AttnWork& w, uint16_t* att, hipStream_t st) {
-  if (d > 128 || d % 16) return fail(MC_E_INVALID, "attention: head_dim must be a multiple of 16 and <= 128");
+  if (d != 64 && d != 128) return fail(MC_E_INVALID, "attention: head_dim must be 64 or 128");
   (void)max_q;
   const float scale = 1.0f / sqrtf((float)d);
-  if (d == 64 || d == 128) {
-    // 64-key sub-chunks per block: at least one per wave, more when the grid would exceed
-    // about 1024 blocks (fewer partials to merge)
-    const int S = std::max(4, (R * nkv * w.nchunk + 1023) / 1024);
-    const dim3 grid(R * nkv, (w.nchunk + S - 1) / S);
-    if (d == 128) hipLaunchKernelGGL(attn_flash_kernel<128>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
-    else hipLaunchKernelGGL(attn_flash_kernel<64>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
-    MC_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((M * nq + 3) / 4), dim3(256), 0, st, sv, M, nq, d, S, w, att);
-    MC_HIP(hipGetLastError());
-    return MC_OK;
-  }
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(R * nkv, w.nchunk), dim3(256), 0, st, q, kv, sv, nq, nkv, d, scale, w);
+  // 64-key sub-chunks per block: at least one per wave, more when the grid would exceed
+  // about 1024 blocks (fewer partials to merge)
+  const int S = std::max(4, (R * nkv * w.nchunk + 1023) / 1024);
+  const dim3 grid(R * nkv, (w.nchunk + S - 1) / S);
+  if (d == 128) hipLaunchKernelGGL(attn_flash_kernel<128>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
+  else hipLaunchKernelGGL(attn_flash_kernel<64>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
   MC_HIP(hipGetLastError());
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((M * nq + 3) / 4), dim3(256), 0, st, sv, M, nq, d, w, att);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((M * nq + 3) / 4), dim3(256), 0, st, sv, M, nq, d, S, w, att);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }

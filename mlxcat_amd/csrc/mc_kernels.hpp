@@ -32,7 +32,7 @@ int launch_embed(const QLinear& E, const int32_t* slot_tok, int M, int H, uint16
 int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uint16_t* k_norm, const float* rope_cos,
                           const float* rope_sin, int M, int nq, int nkv, int d, float eps, const int32_t* slot_row,
                           const int32_t* slot_pos, KVLayer kv, uint16_t* q_out, hipStream_t st);
-// split-KV attention: partials then combine into att [M][nq d]
+// split-KV attention (head_dim 64 or 128): per-split partials, then their merge into att [M][nq d]
 struct AttnWork {
   float* part_o;   // [M][nq][nchunk][d]
   float* part_ml;  // [M][nq][nchunk][2]
