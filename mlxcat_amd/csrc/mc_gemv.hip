@@ -483,7 +483,8 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
 
   // ---- small loads first (vmcnt retires in order): norm partials, norm weights, the first
   // pass of X; then the first unit's weights ----
-  constexpr int XCH = 4;
+  constexpr int XCH = 4;                 // chunks per thread and staging batch
+  constexpr int XALL = 4 * XCH;          // every chunk of X: Mr x kr x 16 <= 64 x 8 x 16 = 16 x 512
   // norm partials: rows wave + 8 j (j < 8 covers Mr <= 64), producer tiles lane + 64 q (ss_nt <= 256)
   float ssq[8][4];
   if (a.norm_w) {
@@ -497,9 +498,10 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
   }
   u32x4 nw = {0u, 0u, 0u, 0u};
   if (a.norm_w && tid < cpr && k0 + tid * 8 < a.K) nw = *reinterpret_cast<const u32x4*>(a.norm_w + k0 + tid * 8);
-  u32x4 xv[XCH];
+  // all of X before the weights (vmcnt retires in order: the staging below then waits for X only)
+  u32x4 xv[XALL];
 #pragma unroll
-  for (int q = 0; q < XCH; ++q) {
+  for (int q = 0; q < XALL; ++q) {
     const int i = tid + MID_THREADS * q;
     xv[q] = (u32x4){0u, 0u, 0u, 0u};
     if (i < xtotal) {
@@ -525,18 +527,11 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
   }
 
   // ---- X (normalised) into LDS with its group sums ----
-  for (int base = 0; base < xtotal; base += MID_THREADS * XCH) {
-    if (base > 0) {
 #pragma unroll
-      for (int q = 0; q < XCH; ++q) {
-        const int i = base + tid + MID_THREADS * q;
-        xv[q] = (u32x4){0u, 0u, 0u, 0u};
-        if (i < xtotal) {
-          const int m = (int)__umulhi((unsigned)i, cpr_magic), ch = i - m * cpr;
-          if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
-        }
-      }
-    }
+  for (int bq = 0; bq < XALL / XCH; ++bq) {
+    const int base = bq * MID_THREADS * XCH;
+    if (base >= xtotal) break;
+    u32x4* xb = xv + bq * XCH;
     int mm[XCH], cc[XCH];
     bool in[XCH];
 #pragma unroll
@@ -558,20 +553,20 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
       for (int q = 0; q < XCH; ++q)
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-          const float lo = (__uint_as_float(xv[q][h] << 16) * rr[q]) * __uint_as_float(ww[q][h] << 16);
-          const float hi = (__uint_as_float(xv[q][h] & 0xFFFF0000u) * rr[q]) * __uint_as_float(ww[q][h] & 0xFFFF0000u);
-          xv[q][h] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+          const float lo = (__uint_as_float(xb[q][h] << 16) * rr[q]) * __uint_as_float(ww[q][h] << 16);
+          const float hi = (__uint_as_float(xb[q][h] & 0xFFFF0000u) * rr[q]) * __uint_as_float(ww[q][h] & 0xFFFF0000u);
+          xb[q][h] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
         }
     }
     float gs[XCH];
 #pragma unroll
     for (int q = 0; q < XCH; ++q) {
-      if (in[q]) *reinterpret_cast<u32x4*>(xl + mm[q] * XS + cc[q] * 8) = xv[q];
+      if (in[q]) *reinterpret_cast<u32x4*>(xl + mm[q] * XS + cc[q] * 8) = xb[q];
       float s0 = 0.f, s1 = 0.f;
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
-        s0 += __uint_as_float(xv[q][h] << 16);
-        s1 += __uint_as_float(xv[q][h] & 0xFFFF0000u);
+        s0 += __uint_as_float(xb[q][h] << 16);
+        s1 += __uint_as_float(xb[q][h] & 0xFFFF0000u);
       }
       gs[q] = in[q] ? s0 + s1 : 0.f;
     }
