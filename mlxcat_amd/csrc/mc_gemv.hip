@@ -209,12 +209,9 @@ __device__ inline void store_partial(const GemvArgs& a, const f32x4 (&acc)[MT], 
 
 // Count this wave's arrival for tile t (its partial stores are complete); the last of the
 // ksplit arrivals sums the partials in K-range order and runs the epilogue.
+// The last arrival of tile t: sum its partials in K-range order, rearm the counter, epilogue.
 template <int MT>
-__device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16) {
-  unsigned arrived = 0u;
-  if (lane == 0) arrived = atomicAdd(a.counters + t, 1u);
-  arrived = __shfl(arrived, 0);
-  if (arrived != (unsigned)(a.ksplit - 1)) return;
+__device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, int r16) {
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -231,6 +228,33 @@ __device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16
   }
   if (lane == 0) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   epilogue<MT>(a, acc, t, c, r16);
+}
+
+template <int MT>
+__device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16) {
+  unsigned arrived = 0u;
+  if (lane == 0) arrived = atomicAdd(a.counters + t, 1u);
+  arrived = __shfl(arrived, 0);
+  if (arrived != (unsigned)(a.ksplit - 1)) return;
+  finish_tile<MT>(a, t, lane, c, r16);
+}
+
+// Arrivals of a wave's units t0, t0 + ts, ... < NT, 64 at a time: lane i counts unit i (the
+// atomics of all units are in flight together), then the wave finishes the tiles whose
+// last arrival it was.
+template <int MT>
+__device__ inline void arrive_units(const GemvArgs& a, int t0, int ts, int lane, int c, int r16) {
+  for (int b = t0; b < a.NT; b += 64 * ts) {
+    const int t = b + lane * ts;
+    unsigned arrived = 0u;
+    if (t < a.NT) arrived = atomicAdd(a.counters + t, 1u);
+    unsigned long long last = __ballot(t < a.NT && arrived == (unsigned)(a.ksplit - 1));
+    while (last) {
+      const int i = __ffsll((long long)last) - 1;
+      last &= last - 1;
+      finish_tile<MT>(a, b + i * ts, lane, c, r16);
+    }
+  }
 }
 
 // U work units per block: unit u = tile (u / ksplit) x K-range (u % ksplit); block b takes
@@ -610,7 +634,7 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
   if (deferred) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
-    for (int tt = t0; tt < a.NT; tt += tstride) arrive<MT>(a, tt, lane, c, r16);
+    arrive_units<MT>(a, t0, tstride, lane, c, r16);
   }
 }
 

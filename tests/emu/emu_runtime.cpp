@@ -84,7 +84,7 @@ struct Lane {
   int block = 0, wave = 0, lane = 0;
   bool done = false;
 };
-enum { K_NONE, K_SHFL_F, K_SHFL_I, K_SHFL_U64, K_SHFL_U, K_ANY, K_SYNC, K_MFMA, K_MFMA16 };
+enum { K_NONE, K_SHFL_F, K_SHFL_I, K_SHFL_U64, K_SHFL_U, K_ANY, K_BALLOT, K_SYNC, K_MFMA, K_MFMA16 };
 struct Wave {
   int kind = K_NONE, arrived = 0;
   unsigned gen = 0;
@@ -189,6 +189,17 @@ int any(int pred) {
     for (int k = 0; k < 64; ++k) w.io[k] = a;
   });
   return W.io[l];
+}
+unsigned long long ballot(int pred) {
+  Wave& W = my_wave();
+  const int l = my_lane();
+  W.i[l] = pred != 0;
+  arrive(W, K_BALLOT, [](Wave& w) {
+    unsigned long long m = 0;
+    for (int k = 0; k < 64; ++k) m |= (unsigned long long)(w.i[k] != 0) << k;
+    for (int k = 0; k < 64; ++k) w.qo[k] = m;
+  });
+  return W.qo[l];
 }
 void wave_sync() {
   arrive(my_wave(), K_SYNC, [](Wave&) {});

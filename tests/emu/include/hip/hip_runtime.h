@@ -117,6 +117,7 @@ int shfl_xor_i(int v, int mask);
 unsigned long long shfl_xor_u64(unsigned long long v, int mask);
 unsigned shfl_u(unsigned v, int src);
 int any(int pred);
+unsigned long long ballot(int pred);
 void wave_sync();
 void block_sync();
 void spin_yield();
@@ -174,6 +175,8 @@ inline int emu_dpp(int src, int ctrl) {
 }
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((src), (ctrl))
 inline int __any(int pred) { return emu::any(pred); }
+inline unsigned long long __ballot(int pred) { return emu::ballot(pred); }
+inline int __ffsll(long long x) { return __builtin_ffsll(x); }
 inline void __syncthreads() { emu::block_sync(); }
 inline unsigned long long wall_clock64() { return emu::clock(); }
 inline float __expf(float x) { return expf(x); }
