@@ -114,6 +114,81 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forward_mode: int
     return out
 
 
+def moe_step_bytes(cfg: dict, ctx_lens, M: int) -> float:
+    """Algorithmic bytes of a Qwen3-MoE verify step: attention projections, router and the
+    expected number of distinct experts M tokens touch under uniform routing,
+    E (1 - (1 - k/E)^M), per layer; K/V and logits as for the dense decoder."""
+    H, d, nq, nkv, V, L = (cfg[k] for k in ("hidden", "head_dim", "n_q_heads", "n_kv_heads", "vocab", "n_layers"))
+    E, TK, MI = cfg["n_experts"], cfg["n_experts_per_tok"], cfg["moe_intermediate"]
+    touched = E * (1.0 - (1.0 - TK / E) ** M)
+    per_layer = (nq + 2 * nkv) * d * H + H * nq * d + E * H + touched * 3 * MI * H
+    weights = (L * per_layer + V * H) * 0.5625
+    kv_tok = L * 2 * nkv * d * 2
+    return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
+
+
+# The survey's other workloads (parity-tested; measured here on demand, not the headline):
+# (model, rows, K, context lengths (lo, hi), sampling per row, forced accept-length schedule)
+CONFIGS = {
+    "cfg3": ("llama3-8b", 8, 4, (512, 4096), "t0.7-topp0.95", False),
+    "cfg4": ("qwen3-30b-a3b", 4, 4, (1024, 1024), "greedy", False),
+    "cfg5": ("qwen3-8b", 32, 8, (16384, 16384), "even-greedy-odd-seeded", True),
+}
+
+
+def run_config(name: str, steps: int, warmup: int) -> dict:
+    """One of CONFIGS: synthetic K/V for each row's context, seeded copy-span prompts, then
+    speculative steps (a forced accept length uniform in [0, K] per row per step where the
+    configuration asks for it)."""
+    from mlxcat_amd import _lib as hip
+    from mlxcat_amd.workloads import MODELS, copy_span_prompt
+    model, rows, k, (lo, hi), samp, forced = CONFIGS[name]
+    cfg = MODELS[model]
+    L = hip.load()
+    if L.mc_set_device(0) < 0:
+        raise RuntimeError(L.mc_last_error().decode())
+    m = hip.Model(cfg)
+    m.init_synthetic(SEED)
+    rng = np.random.default_rng(SEED)
+    lens = [int(x) for x in rng.integers(lo, hi + 1, rows)]
+    max_new = (warmup + steps + 4) * (k + 1) + 8
+    spec = dict(enabled=1, max_proposal_tokens=k, max_suffix_tokens=MATCH, min_context_tokens=8, acceptance=1,
+                single_row_only=0, greedy_only=0)
+    b = hip.Batch(m, rows, max(lens) + max_new + k + 16, spec)
+    b.set_fused(0)
+    for r in range(rows):
+        if samp == "greedy" or (samp == "even-greedy-odd-seeded" and r % 2 == 0):
+            sp = hip.make_sampling()
+        elif samp == "even-greedy-odd-seeded":
+            sp = hip.make_sampling(temperature=0.7, top_p=0.95, seed=SEED + r)
+        else:
+            sp = hip.make_sampling(temperature=0.7, top_p=0.95, seed=SEED + r)
+        b.fill_synthetic_kv(r, lens[r] - 1, 99 + r)
+        b.insert_prefilled(r, copy_span_prompt(SEED + r, lens[r], cfg["vocab"]), max_new, sp)
+    fa = (lambda: rng.integers(0, k + 1, rows).astype(np.int32)) if forced else (lambda: None)
+    for _ in range(warmup):
+        b.step(fa())
+    kv0 = [b.kv_len(r) for r in range(rows)]
+    emitted = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, c, _ = b.step(fa())
+        emitted += int(c.sum())
+    dt = time.perf_counter() - t0
+    M = rows * (k + 1)
+    by = moe_step_bytes(cfg, kv0, M) if cfg["n_experts"] else step_bytes(cfg, kv0, M)
+    ms = dt / steps * 1e3
+    b.close()
+    m.close()
+    return {"config": {"workload": f"{model}-shape 4-bit g64 n-gram speculative step", "batch": rows, "k_draft": k,
+                       "context": [lo, hi], "sampling": samp, "forced_accept_schedule": forced},
+            "value": round(emitted / dt, 2), "unit": "tok/s", "ms_per_step": round(ms, 4), "steps": steps,
+            "warmup": warmup, "tokens_per_step_per_row": round(emitted / steps / rows, 3), "verify_tokens": M,
+            "verify_step_hbm": {"achieved": round(by / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_step": by},
+            "dtype": "bf16", "data": "synthetic (random-init weights, synthetic K/V, seeded copy-span prompts)"}
+
+
 def run_cpu(budget_s: float = 20.0):
     """The oracle (CPU restatement, OpenMP) on a bounded sample of the same batch-1 step:
     synthetic K/V for the 2047 prefilled positions, then speculative steps until the
@@ -151,6 +226,8 @@ def main():
     ap.add_argument("--forward", choices=["multi", "persistent", "auto"], default="multi",
                     help="verify forward: the per-layer kernels (the faster path on MI355X today), the persistent "
                          "forward kernel (required), or the persistent kernel whenever the shape allows it")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default=None,
+                    help="measure one of the other workloads instead (its own JSON line)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="only copy 256 MiB three times (a plain copy kernel of known size: the scale of the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -165,6 +242,14 @@ def main():
         print("copied 3 x 256 MiB", flush=True)
         return
     mode = {"auto": 1, "persistent": 2, "multi": 0}[a.forward]
+    if a.config:
+        if a.gpus != 1:
+            print("bench.py measures one GPU", file=sys.stderr)
+            sys.exit(2)
+        out = run_config(a.config, max(3, a.steps // 4), max(2, a.warmup // 2))
+        out.update({"metric": f"accepted tok/s ({a.config})", "n_gpus": 1, "higher_is_better": True})
+        print(json.dumps(out), flush=True)
+        return
     if a.gpus != 1:
         print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
