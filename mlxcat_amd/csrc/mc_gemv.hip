@@ -805,14 +805,18 @@ static int setup_mt() {
 // ---------------------------------------------------------------------------------------
 constexpr int MOE_MAX_GP = 20;  // K <= 2560
 
+constexpr int MOE_ROWS = 8;  // routed pairs staged at a time (a verify block routes ~1-3 per expert)
+
 __host__ __device__ constexpr size_t moe_lds_bytes(int GP) {
-  return (size_t)16 * xrow_stride(GP) * 2 + (size_t)16 * 2 * GP * 4 + (size_t)2 * GEMV_WAVES * 64 * 16;
+  return (size_t)MOE_ROWS * xrow_stride(GP) * 2 + (size_t)16 * 2 * GP * 4;
 }
 
-// Block (slot, jb): touched expert act_e[slot], tiles jb, jb + nb, ... with the full K range.
-// The expert's pairs are taken 16 at a time (one m-tile); for each such group the block
-// stages the pairs' input rows and streams its tiles, the next tile's weights in flight
-// while the current one is computed.
+// Block (slot, jb): touched expert act_e[slot], tiles jb, jb + nb, ... with the full K range;
+// wave w of the block takes the block's tiles w, w + 4, ..., each as K-chunks of up to D
+// group pairs accumulated in order, so the wave needs no partner to finish a tile and keeps
+// the next chunk's weights (D KiB) in flight while it computes the current one.  The
+// expert's pairs are taken MOE_ROWS at a time (rows of one m-tile; the LDS they need lets
+// four blocks share a CU); for each such group the block stages the pairs' input rows.
 template <int D>
 __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
   MC_DYN_LDS(smem);
@@ -821,9 +825,9 @@ __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
   const int e = a.rt.act_e[slot];
   const int p0 = a.rt.off[slot], np = a.rt.off[slot + 1] - p0;
   const int GP = a.GP, XS = xrow_stride(GP), cpr = GP * 16, ng = 2 * GP;
-  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                      // [16][XS]
-  float* xsum = reinterpret_cast<float*>(smem + (size_t)16 * XS * 2);    // [2 GP][16]
-  float* red = xsum + 16 * ng;                                           // [2][4][64][4]
+  const int nkc = (GP + D - 1) / D;  // K-chunks per tile
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                            // [MOE_ROWS][XS]
+  float* xsum = reinterpret_cast<float*>(smem + (size_t)MOE_ROWS * XS * 2);    // [2 GP][16]
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane >> 4, r16 = lane & 15;
   GemvArgs g;  // the expert's weights, for load_unit
   g.qw = a.qw + (size_t)e * a.qw_es;
@@ -833,12 +837,18 @@ __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
   const uint32_t mask = a.dq_mask;
   uint32_t magic;
   MC_TO_VGPR(magic, a.dq_magic);
-  for (int q0 = 0; q0 < np; q0 += 16) {
-    const int Mr = min(16, np - q0);
-    int step = 0;  // weight buffer and reduction buffer parity, reduction wave
-    // the first tile's weights, then the pairs' input rows into LDS
+  const int tstride = GEMV_WAVES * a.nb;
+  const int t0 = jb + a.nb * wave;
+  // units of this wave: u = tile index i (t = t0 + i tstride) x K-chunk kc, in order
+  const int ntl = t0 < a.NT ? (a.NT - t0 + tstride - 1) / tstride : 0;
+  const int nunits = ntl * nkc;
+  auto unit_tile = [&](int u) { return t0 + (u / nkc) * tstride; };
+  auto unit_gp0 = [&](int u) { return (u % nkc) * D; };
+  auto unit_ngp = [&](int u) { return min(GP, unit_gp0(u) + D) - unit_gp0(u); };
+  for (int q0 = 0; q0 < np; q0 += MOE_ROWS) {
+    const int Mr = min(MOE_ROWS, np - q0);  // MFMA rows >= Mr read row Mr - 1 and are not stored
     WBuf<D> wa, wb;
-    load_unit<D>(wa, g, jb, 0, GP, wave, lane, r16);
+    if (nunits > 0) load_unit<D, 1>(wa, g, unit_tile(0), unit_gp0(0), unit_ngp(0), 0, lane, r16);
     for (int i0 = 0; i0 < Mr * cpr; i0 += 256 * 4) {
       u32x4 v[4];
       int mm[4], cc[4];
@@ -876,32 +886,41 @@ __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
     if (lane < 16 - Mr)
       for (int gl = wave; gl < ng; gl += GEMV_WAVES) xsum[gl * 16 + Mr + lane] = 0.f;
     lds_barrier();
-    for (int t = jb; t < a.NT; t += a.nb, ++step) {
-      const bool odd = (step & 1) != 0;
-      WBuf<D>& cur = odd ? wb : wa;
-      WBuf<D>& nxt = odd ? wa : wb;
-      const int tn = t + a.nb < a.NT ? t + a.nb : t;  // the last tile re-reads itself
-      load_unit<D>(nxt, g, tn, 0, GP, wave, lane, r16);
-      f32x4 acc[1];
-      compute_unit<1, D>(acc, cur, xl, xsum, XS, Mr, GP, wave, c, r16, mask, magic);
-      float* rb = red + (size_t)(step & 1) * GEMV_WAVES * 64 * 4;
-      *reinterpret_cast<f32x4*>(rb + (wave * 64 + lane) * 4) = acc[0];
-      lds_barrier();
-      if (wave == (step & 3)) {
-        reduce_waves<1>(acc, rb, lane);
-        const int n = t * 16 + r16;
+    f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+    auto finish = [&](int u, const WBuf<D>& cur) {
+      f32x4 part[1];
+      // the chunk's pairs: compute_unit indexes the staged X from pair 0 of the K range
+      compute_unit<1, D, 1>(part, cur, xl + unit_gp0(u) * 128, xsum + unit_gp0(u) * 2 * 16, XS, Mr, unit_ngp(u), 0, c,
+                            r16, mask, magic);
+      acc[0] += part[0];
+      if (u % nkc != nkc - 1) return;
+      const int t = unit_tile(u);
+      const int n = t * 16 + r16;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = 4 * c + v;
-          const bool live = m < Mr;
-          const int pr = live ? a.rt.pairs[p0 + q0 + m] : 0;
-          if (a.epi == EPI_SWIGLU) {
-            const float up = __shfl_xor(acc[0][v], 1);
-            if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)pr * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[0][v]) * up);
-          } else if (live && n < a.N) {
-            a.yf[(size_t)pr * a.ldy + n] = acc[0][v];
-          }
+      for (int v = 0; v < 4; ++v) {
+        const int m = 4 * c + v;
+        const bool live = m < Mr;
+        const int pr = live ? a.rt.pairs[p0 + q0 + m] : 0;
+        if (a.epi == EPI_SWIGLU) {
+          const float up = __shfl_xor(acc[0][v], 1);
+          if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)pr * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[0][v]) * up);
+        } else if (live && n < a.N) {
+          a.yf[(size_t)pr * a.ldy + n] = acc[0][v];
         }
+      }
+      acc[0] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    for (int u = 0; u < nunits; u += 2) {
+      {
+        const int un = u + 1 < nunits ? u + 1 : u;  // the last unit re-reads itself
+        load_unit<D, 1>(wb, g, unit_tile(un), unit_gp0(un), unit_ngp(un), 0, lane, r16);
+        finish(u, wa);
+      }
+      if (u + 1 >= nunits) break;
+      {
+        const int un = u + 2 < nunits ? u + 2 : u + 1;
+        load_unit<D, 1>(wa, g, unit_tile(un), unit_gp0(un), unit_ngp(un), 0, lane, r16);
+        finish(u + 1, wb);
       }
     }
     // the staged rows are rewritten by the next group: every wave is past its last tile
@@ -920,13 +939,10 @@ int moe_gemv_launch(const MoeGemvArgs& a, hipStream_t st) {
     return fail(MC_E_INVALID, "moe gemv: epilogue");
   const size_t lds = moe_lds_bytes(a.GP);
   const dim3 grid((unsigned)(a.max_active * a.nb));
-  switch ((a.GP + GEMV_WAVES - 1) / GEMV_WAVES) {
-    case 1: hipLaunchKernelGGL(moe_gemv_kernel<1>, grid, dim3(256), lds, st, a); break;
-    case 2: hipLaunchKernelGGL(moe_gemv_kernel<2>, grid, dim3(256), lds, st, a); break;
-    case 3: hipLaunchKernelGGL(moe_gemv_kernel<3>, grid, dim3(256), lds, st, a); break;
-    case 4: hipLaunchKernelGGL(moe_gemv_kernel<4>, grid, dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL(moe_gemv_kernel<5>, grid, dim3(256), lds, st, a); break;
-  }
+  // K-chunks of up to 8 group pairs (the largest unit a wave keeps in registers)
+  if (a.GP <= 4) hipLaunchKernelGGL(moe_gemv_kernel<4>, grid, dim3(256), lds, st, a);
+  else if (a.GP <= 6) hipLaunchKernelGGL(moe_gemv_kernel<6>, grid, dim3(256), lds, st, a);
+  else hipLaunchKernelGGL(moe_gemv_kernel<8>, grid, dim3(256), lds, st, a);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
@@ -1099,8 +1115,7 @@ int gemv_setup_lds() {
                        (const void*)qgemv_mid_kernel<4, 4>, (const void*)qgemv_mid_kernel<4, 6>,
                        (const void*)qgemv_mid_kernel<4, 8>};
   for (const void* f : mid) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, MID_LDS_CAP));
-  const void* moe[] = {(const void*)moe_gemv_kernel<1>, (const void*)moe_gemv_kernel<2>, (const void*)moe_gemv_kernel<3>,
-                       (const void*)moe_gemv_kernel<4>, (const void*)moe_gemv_kernel<5>};
+  const void* moe[] = {(const void*)moe_gemv_kernel<4>, (const void*)moe_gemv_kernel<6>, (const void*)moe_gemv_kernel<8>};
   for (const void* f : moe)
     MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)moe_lds_bytes(MOE_MAX_GP)));
   return MC_OK;
