@@ -812,8 +812,8 @@ __host__ __device__ constexpr size_t moe_lds_bytes(int GP) {
 }
 
 // Block (slot, jb): touched expert act_e[slot], tiles jb, jb + nb, ... with the full K range;
-// wave w of the block takes the block's tiles w, w + 4, ..., each as K-chunks of up to D
-// group pairs accumulated in order, so the wave needs no partner to finish a tile and keeps
+// wave w of the block takes the block's tiles w, w + 4, ..., each as K-chunks of D group
+// pairs accumulated in order, so the wave needs no partner to finish a tile and keeps
 // the next chunk's weights (D KiB) in flight while it computes the current one.  The
 // expert's pairs are taken MOE_ROWS at a time (rows of one m-tile; the LDS they need lets
 // four blocks share a CU); for each such group the block stages the pairs' input rows.
@@ -939,10 +939,8 @@ int moe_gemv_launch(const MoeGemvArgs& a, hipStream_t st) {
     return fail(MC_E_INVALID, "moe gemv: epilogue");
   const size_t lds = moe_lds_bytes(a.GP);
   const dim3 grid((unsigned)(a.max_active * a.nb));
-  // K-chunks of up to 8 group pairs (the largest unit a wave keeps in registers)
-  if (a.GP <= 4) hipLaunchKernelGGL(moe_gemv_kernel<4>, grid, dim3(256), lds, st, a);
-  else if (a.GP <= 6) hipLaunchKernelGGL(moe_gemv_kernel<6>, grid, dim3(256), lds, st, a);
-  else hipLaunchKernelGGL(moe_gemv_kernel<8>, grid, dim3(256), lds, st, a);
+  // K-chunks of 4 group pairs: registers for three blocks per CU (measured faster than 8)
+  hipLaunchKernelGGL(moe_gemv_kernel<4>, grid, dim3(256), lds, st, a);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
@@ -1115,7 +1113,7 @@ int gemv_setup_lds() {
                        (const void*)qgemv_mid_kernel<4, 4>, (const void*)qgemv_mid_kernel<4, 6>,
                        (const void*)qgemv_mid_kernel<4, 8>};
   for (const void* f : mid) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, MID_LDS_CAP));
-  const void* moe[] = {(const void*)moe_gemv_kernel<4>, (const void*)moe_gemv_kernel<6>, (const void*)moe_gemv_kernel<8>};
+  const void* moe[] = {(const void*)moe_gemv_kernel<4>};
   for (const void* f : moe)
     MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)moe_lds_bytes(MOE_MAX_GP)));
   return MC_OK;
