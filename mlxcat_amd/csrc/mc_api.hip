@@ -411,6 +411,7 @@ struct mc_batch {
   size_t gemv_part_n = 0;  // floats
   int gemv_cnt_n = 0;
   float* ssq = nullptr;  // [Mmax][hidden / 16]: per-tile sums of squares of the residual stream
+  uint16_t* xn = nullptr;  // [Mmax][hidden]: normalised rows for the M > 64 GEMM (allocated when Mmax > 64)
   unsigned long long* amax = nullptr;  // [Mmax][vocab tiles]: greedy argmax partials of the head
   // Qwen3-MoE: normalised rows, router logits, routing, per-pair expert outputs
   uint16_t *moe_xn = nullptr, *moe_logits = nullptr, *moe_act = nullptr;
@@ -464,7 +465,7 @@ static void batch_free(mc_batch* b) {
                   (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
                   (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll, (void*)b->xf_args,
                   (void*)b->moe_xn, (void*)b->moe_logits, (void*)b->moe_act, (void*)b->moe_out, (void*)b->moe_i32,
-                  (void*)b->moe_wts})
+                  (void*)b->moe_wts, (void*)b->xn})
     if (p) (void)hipFree(p);
   if (b->h_i32) (void)hipHostFree(b->h_i32);
   if (b->h_out) (void)hipHostFree(b->h_out);
@@ -728,7 +729,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     b->gemv_part_n = part;
     b->gemv_cnt_n = maxnt;
     if ((rc = dev_alloc(&b->gemv_part, part)) || (rc = dev_zero(&b->gemv_cnt, (size_t)maxnt)) ||
-        (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M)) ||
+        (rc = dev_zero(&b->ssq, (size_t)(H / 16) * M)) || (M > 64 && (rc = dev_zero(&b->xn, (size_t)M * H))) ||
         (rc = dev_zero(&b->amax, (size_t)M * m->head().NT))) {
       batch_free(b);
       return rc;
@@ -877,6 +878,30 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
                     int ldy, int M, int epi, int ss_m0 = 0, unsigned long long* amax = nullptr) {
   const auto& c = b->m->cfg;
   const int H = c.hidden;
+  if (M > 64) {  // one GEMM over every token (the input rows normalised first when the linear has a norm)
+    const uint16_t* xin = x;
+    int ldxin = ldx;
+    int rc;
+    if (norm_w) {
+      if ((rc = launch_rows_rmsnorm(x, norm_w, M, H, c.rms_eps, b->xn, b->st))) return rc;
+      xin = b->xn;
+      ldxin = H;
+    }
+    GemvArgs a;
+    a.qw = L.qw; a.sb = L.sb;
+    a.x = xin; a.ldx = ldxin;
+    if (epi == EPI_RESIDUAL) {
+      a.ss_out = b->ssq + (size_t)ss_m0 * (H / 16); a.ss_ld_out = H / 16;
+    }
+    a.y = y; a.ldy = ldy;
+    a.M = M; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
+    a.epi = epi;
+    a.amax = amax;
+    size_t e0 = 0;
+    if ((rc = prof_begin(b, &e0))) return rc;
+    if ((rc = qgemm_launch(a, b->st))) return rc;
+    return prof_end(b, e0, 0, L.alg_bytes());
+  }
   for (int m0 = 0; m0 < M; m0 += 64) {
     const int mc = std::min(64, M - m0);
     const int MT = (mc + 15) / 16;

@@ -638,6 +638,169 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// GEMM for M > 64 (verify blocks of many rows): the weights are dequantised once per K-step
+// and used against every token tile of the block
+// ---------------------------------------------------------------------------------------
+// Block (n-block, m-block): 128 weight rows (wave w owns tiles 8 nb + 2 w, + 1) x 16 MB
+// tokens, accumulators resident over the whole K.  The activations go through LDS one
+// 128-wide K-step (group pair) at a time, double-buffered: the next step's loads are in
+// flight while the current step is computed, and its group sums are formed as it is
+// written.  The input rows are already normalised (no fused RMSNorm here).
+constexpr int QG_MB = 6;                 // token tiles per block (96 tokens)
+constexpr int QG_NTW = 2;                // weight tiles per wave
+constexpr int QG_XS = 128 + 8;           // LDS row stride (bf16) of one K-step of X
+constexpr int QG_XCH = QG_MB * 16 * 16 / 256;  // 16-byte X chunks per thread per K-step
+
+size_t qgemm_lds_bytes() { return (size_t)2 * 16 * QG_MB * QG_XS * 2 + (size_t)2 * 2 * 16 * QG_MB * 4; }
+
+__global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
+  MC_DYN_LDS(smem);
+  constexpr int MR = 16 * QG_MB;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                          // [2][MR][QG_XS]
+  float* xsum = reinterpret_cast<float*>(smem + (size_t)2 * MR * QG_XS * 2);  // [2][2 groups][MR]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane >> 4, r16 = lane & 15;
+  const int m0 = blockIdx.y * MR;
+  const int Mb = min(MR, a.M - m0);  // live tokens of this block
+  const int tw = blockIdx.x * 4 * QG_NTW + wave * QG_NTW;  // this wave's first weight tile
+  const int GP = a.GP;
+
+  // X chunk q of a K-step: token row (tid + 256 q) / 16, 16-byte chunk (tid + 256 q) % 16
+  auto load_x = [&](int gp, u32x4 (&xv)[QG_XCH]) {
+#pragma unroll
+    for (int q = 0; q < QG_XCH; ++q) {
+      const int i = tid + 256 * q, m = i >> 4, ch = i & 15;
+      xv[q] = (u32x4){0u, 0u, 0u, 0u};
+      if (m < Mb && gp * 128 + ch * 8 < a.K)
+        xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)(m0 + m) * a.ldx + gp * 128 + ch * 8);
+    }
+  };
+  auto store_x = [&](int buf, const u32x4 (&xv)[QG_XCH]) {
+    uint16_t* xb = xl + (size_t)buf * MR * QG_XS;
+    float* sb = xsum + (size_t)buf * 2 * MR;
+    float gs[QG_XCH];
+#pragma unroll
+    for (int q = 0; q < QG_XCH; ++q) {
+      const int i = tid + 256 * q, m = i >> 4, ch = i & 15;
+      *reinterpret_cast<u32x4*>(xb + m * QG_XS + ch * 8) = xv[q];
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        s0 += __uint_as_float(xv[q][h] << 16);
+        s1 += __uint_as_float(xv[q][h] & 0xFFFF0000u);
+      }
+      gs[q] = s0 + s1;
+    }
+#pragma unroll
+    for (int q = 0; q < QG_XCH; ++q) gs[q] = sum8_lanes(gs[q]);
+#pragma unroll
+    for (int q = 0; q < QG_XCH; ++q) {
+      const int i = tid + 256 * q, m = i >> 4, ch = i & 15;
+      if ((ch & 7) == 0) sb[(ch >> 3) * MR + m] = gs[q];
+    }
+  };
+  // weights of K-step gp for the wave's tiles (a tile past the end re-reads the last one)
+  auto load_w = [&](int gp, u32x4 (&wq)[QG_NTW], uint2 (&wsb)[QG_NTW]) {
+#pragma unroll
+    for (int n = 0; n < QG_NTW; ++n) {
+      const int t = min(tw + n, a.NT - 1);
+      wq[n] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.qw) + ((size_t)t * GP + gp) * 64 + lane);
+      wsb[n] = reinterpret_cast<const uint2*>(a.sb)[tile_sb_word(t, r16, gp, 0, GP) / 2];
+    }
+  };
+
+  f32x4 acc[QG_NTW][QG_MB];
+#pragma unroll
+  for (int n = 0; n < QG_NTW; ++n)
+#pragma unroll
+    for (int mt = 0; mt < QG_MB; ++mt) acc[n][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const uint32_t mask = a.dq_mask;
+  uint32_t magic;
+  MC_TO_VGPR(magic, a.dq_magic);
+
+  // weights of K-steps s .. s + 3 in a ring of registers (slot s % 4, static after the unroll)
+  u32x4 wr[4][QG_NTW];
+  uint2 sr[4][QG_NTW];
+  u32x4 xv[QG_XCH];
+  load_x(0, xv);
+  load_w(0, wr[0], sr[0]);
+  load_w(min(1, GP - 1), wr[1], sr[1]);
+  load_w(min(2, GP - 1), wr[2], sr[2]);
+  store_x(0, xv);
+  lds_barrier();
+  for (int g0 = 0; g0 < GP; g0 += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int gp = g0 + u;
+      if (gp >= GP) break;  // uniform
+      const int buf = gp & 1;
+      // every load unconditional (the last steps re-read themselves), X first: the wait for
+      // X below then leaves the weights of step gp + 3 in flight
+      load_x(min(gp + 1, GP - 1), xv);
+      load_w(min(gp + 3, GP - 1), wr[(u + 3) & 3], sr[(u + 3) & 3]);
+      const u32x4 (&wq0)[QG_NTW] = wr[u];
+      const uint2 (&ws0)[QG_NTW] = sr[u];
+      // ---- compute K-step gp ----
+      const uint16_t* xb = xl + (size_t)buf * MR * QG_XS;
+      const float* sbuf = xsum + (size_t)buf * 2 * MR;
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        bf16x8 wv[QG_NTW][2];
+        float sv[QG_NTW], bv[QG_NTW];
+#pragma unroll
+        for (int n = 0; n < QG_NTW; ++n) {
+          wv[n][0] = dequant_word(gi ? wq0[n].z : wq0[n].x, mask, magic);
+          wv[n][1] = dequant_word(gi ? wq0[n].w : wq0[n].y, mask, magic);
+          const uint32_t sbv = gi ? ws0[n].y : ws0[n].x;
+          sv[n] = DQ_STEP * __uint_as_float(sbv << 16);
+          bv[n] = __uint_as_float(sbv & 0xFFFF0000u) - sv[n];
+        }
+#pragma unroll
+        for (int mt = 0; mt < QG_MB; ++mt) {
+          const uint16_t* xrow = xb + (mt * 16 + r16) * QG_XS + gi * 64 + 8 * c;
+          const bf16x8 xa0 = *reinterpret_cast<const bf16x8*>(xrow);
+          const bf16x8 xa1 = *reinterpret_cast<const bf16x8*>(xrow + 32);
+          const f32x4 xs = *reinterpret_cast<const f32x4*>(sbuf + gi * MR + mt * 16 + 4 * c);
+#pragma unroll
+          for (int n = 0; n < QG_NTW; ++n) {
+            f32x4 g = {0.f, 0.f, 0.f, 0.f};
+            g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa0, wv[n][0], g, 0, 0, 0);
+            g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa1, wv[n][1], g, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              acc[n][mt][v] = __builtin_fmaf(sv[n], g[v], acc[n][mt][v]);
+              acc[n][mt][v] = __builtin_fmaf(bv[n], xs[v], acc[n][mt][v]);
+            }
+          }
+        }
+      }
+      if (gp + 1 < GP) store_x(buf ^ 1, xv);  // uniform
+      lds_barrier();  // step gp + 1 is in LDS; step gp's buffer is free for step gp + 2
+    }
+  }
+  // ---- epilogues: this block's tokens m0 .. m0 + Mb - 1 ----
+  GemvArgs e = a;
+  e.M = Mb;
+  e.y = a.y + (size_t)m0 * a.ldy;
+  if (a.amax) e.amax = a.amax + (size_t)m0 * a.NT;
+  if (a.ss_out) e.ss_out = a.ss_out + (size_t)m0 * a.ss_ld_out;
+#pragma unroll
+  for (int n = 0; n < QG_NTW; ++n)
+    if (tw + n < a.NT) epilogue<QG_MB>(e, acc[n], tw + n, c, r16);
+}
+
+int qgemm_launch(const GemvArgs& a, hipStream_t st) {
+  if (a.M <= 64) return fail(MC_E_INVALID, "qgemm: for more than 64 tokens");
+  if (a.K % 64 || a.GP != (a.K + 127) / 128 || a.NT != (a.N + 15) / 16) return fail(MC_E_INVALID, "qgemm: bad shape");
+  if (a.norm_w) return fail(MC_E_INVALID, "qgemm: normalise the input rows first");
+  if (a.amax && a.epi != EPI_STORE) return fail(MC_E_INVALID, "qgemm: argmax partials need the store epilogue");
+  if (a.epi == EPI_RESIDUAL && a.N % 16) return fail(MC_E_INVALID, "qgemm: residual epilogue needs N % 16 == 0");
+  const dim3 grid((unsigned)((a.NT + 4 * QG_NTW - 1) / (4 * QG_NTW)), (unsigned)((a.M + 16 * QG_MB - 1) / (16 * QG_MB)));
+  hipLaunchKernelGGL(qgemm_kernel, grid, dim3(256), qgemm_lds_bytes(), st, a);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
 // K-range plan of the multi-row classes: the largest K-range whose activations fit the LDS
 // cap (at most 8 group pairs), split further (down to 4 pairs) while the units cannot give
 // every wave of the device one.  Depends only on (N, K, MT) and the CU count.

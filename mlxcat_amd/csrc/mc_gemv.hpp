@@ -80,6 +80,9 @@ int launch_moe_combine(uint16_t* x, const float* yd, const float* wts, int M, in
 size_t gemv_lds_bytes(int Mr, int kr, int MT);
 void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit);
 int gemv_launch(const GemvArgs& a, int MT, hipStream_t st);
+// M > 64 tokens: every token tile of a block against each dequantised K-step (input rows
+// already normalised: norm_w must be NULL)
+int qgemm_launch(const GemvArgs& a, hipStream_t st);
 int gemv_setup_lds();
 
 int qlinear_repack(const QLinear& L, int row_off, int row_stride, int Nsrc, const uint32_t* wq_dev,

@@ -10,6 +10,7 @@
 //   case 3: case 0 with 32 q / 8 kv heads, hidden 512 (the XCD-partitioned forward; EMU_CUS=32)
 //   case 4: the case-3 model through mc_step (verify blocks with padding slots; MC_STEP_EAGER=1)
 //   case 5: a small Qwen3-MoE model (16 experts, top-4) through the multi-kernel forward
+//   case 6: the case-0 model, 12 rows: one verify block of 12 x 6 = 72 tokens (the M > 64 GEMM)
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -121,6 +122,46 @@ int main(int argc, char** argv) {
   }
   or_config oc{c.arch, c.n_layers, c.hidden, c.n_q_heads, c.n_kv_heads, c.head_dim, c.intermediate, c.vocab,
                c.tied_embeddings, c.rms_eps, c.rope_theta, c.n_experts, c.n_experts_per_tok, c.moe_intermediate};
+  if (cs == 6) {
+    const int R = 12, W = 6;
+    mc_batch* bb = nullptr;
+    check(mc_batch_create(m, R, ctx, W - 1, &spec, &bb), "batch_create");
+    check(mc_batch_set_fused(bb, 0), "set_fused");
+    or_model* om6 = or_model_create(&oc, SEED, ctx, R);
+    uint64_t rng6 = 0x7777ull;
+    auto toks6 = [&](int n) {
+      std::vector<int32_t> t((size_t)n);
+      for (auto& x : t) { rng6 = or_mix64(rng6); x = (int32_t)(rng6 % (uint64_t)V); }
+      return t;
+    };
+    for (int32_t r = 0; r < R; ++r) {  // prefill: 10 + r tokens per row
+      const int32_t n = 10 + r;
+      auto t = toks6(n);
+      check(mc_forward(bb, 1, &r, &n, t.data(), nullptr), "prefill");
+      or_forward(om6, 1, &r, &n, t.data(), nullptr);
+    }
+    std::vector<int32_t> rows(R), cnts(R, W);
+    for (int r = 0; r < R; ++r) rows[(size_t)r] = r;
+    auto t = toks6(R * W);
+    std::vector<uint16_t> got((size_t)R * W * V), want(got.size());
+    check(mc_forward(bb, R, rows.data(), cnts.data(), t.data(), got.data()), "verify");
+    or_forward(om6, R, rows.data(), cnts.data(), t.data(), want.data());
+    compare("verify 12 x 6 logits", got.data(), want.data(), got.size(), 0);
+    for (int l = 0; l < c.n_layers; ++l)
+      for (int wv = 0; wv < 2; ++wv) {
+        int32_t len = 0;
+        check(mc_batch_kv_len(bb, 11, &len), "kv_len");
+        std::vector<uint16_t> g2((size_t)c.n_kv_heads * len * c.head_dim), w2(g2.size());
+        check(mc_batch_read_kv(bb, l, 11, wv, g2.data()), "read_kv");
+        or_kv_read(om6, l, 11, wv, w2.data());
+        const std::string what = "row 11 kv layer " + std::to_string(l) + (wv ? " V" : " K");
+        compare(what.c_str(), g2.data(), w2.data(), g2.size(), 0);
+      }
+    printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
+    if (emu::oob_loads || emu::oob_stores) ++g_bad;
+    printf("%s\n", g_bad ? "FAIL" : "OK");
+    return g_bad ? 1 : 0;
+  }
   or_model* om = or_model_create(&oc, SEED, ctx, 1);
   uint64_t rng = 0x1234567ull;
   auto tokens = [&](int n) {
