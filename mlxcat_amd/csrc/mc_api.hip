@@ -721,6 +721,13 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
         part = std::max(part, (size_t)ks * L.NT * MT * 64 * 4);
       }
       maxnt = std::max(maxnt, L.NT);
+      if (M > 64) {  // the large-M GEMM's split-K plans
+        size_t qp;
+        int qc;
+        qgemm_workspace(L.NT, L.GP, M, &qp, &qc);
+        part = std::max(part, qp);
+        maxnt = std::max(maxnt, qc);
+      }
     };
     for (auto& L : m->layers)
       for (const QLinear* q : {&L.qkv, &L.o, &L.gateup, &L.down, &L.router})
@@ -897,6 +904,8 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
     a.M = M; a.N = L.N; a.K = L.K; a.NT = L.NT; a.GP = L.GP;
     a.epi = epi;
     a.amax = amax;
+    a.part = b->gemv_part; a.part_floats = b->gemv_part_n;
+    a.counters = b->gemv_cnt; a.counters_n = b->gemv_cnt_n;
     size_t e0 = 0;
     if ((rc = prof_begin(b, &e0))) return rc;
     if ((rc = qgemm_launch(a, b->st))) return rc;

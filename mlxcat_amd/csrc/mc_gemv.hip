@@ -646,11 +646,16 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
 // tokens, accumulators resident over the whole K.  The activations go through LDS one
 // 128-wide K-step (group pair) at a time, double-buffered: the next step's loads are in
 // flight while the current step is computed, and its group sums are formed as it is
-// written.  The input rows are already normalised (no fused RMSNorm here).
+// written.  The input rows are already normalised (no fused RMSNorm here).  When the
+// (weight-block, token-block) grid would leave CUs idle, K is split over blockIdx.z: each
+// K-range leaves device-coherent fp32 partials and the last arrival per tile sums them in
+// K-range order and runs the epilogue (the same protocol as the 17-64-token kernel).
 constexpr int QG_MB = 6;                 // token tiles per block (96 tokens)
 constexpr int QG_NTW = 2;                // weight tiles per wave
+constexpr int QG_RD = 4;                 // K-steps of weights held in registers (prefetch distance QG_RD - 1)
 constexpr int QG_XS = 128 + 8;           // LDS row stride (bf16) of one K-step of X
 constexpr int QG_XCH = QG_MB * 16 * 16 / 256;  // 16-byte X chunks per thread per K-step
+constexpr int QG_KSPLIT_MAX = 8;
 
 size_t qgemm_lds_bytes() { return (size_t)2 * 16 * QG_MB * QG_XS * 2 + (size_t)2 * 2 * 16 * QG_MB * 4; }
 
@@ -664,6 +669,9 @@ __global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
   const int Mb = min(MR, a.M - m0);  // live tokens of this block
   const int tw = blockIdx.x * 4 * QG_NTW + wave * QG_NTW;  // this wave's first weight tile
   const int GP = a.GP;
+  const int kq = blockIdx.z;                                 // K-range: group pairs gq0 .. gq0 + NS - 1
+  const int gq0 = kq * a.kr;
+  const int NS = min(a.GP, gq0 + a.kr) - gq0;                // >= 1 (the plan leaves no empty range)
 
   // X chunk q of a K-step: token row (tid + 256 q) / 16, 16-byte chunk (tid + 256 q) % 16
   auto load_x = [&](int gp, u32x4 (&xv)[QG_XCH]) {
@@ -718,29 +726,29 @@ __global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
   uint32_t magic;
   MC_TO_VGPR(magic, a.dq_magic);
 
-  // weights of K-steps s .. s + 3 in a ring of registers (slot s % 4, static after the unroll)
-  u32x4 wr[4][QG_NTW];
-  uint2 sr[4][QG_NTW];
+  // weights of K-steps s .. s + QG_RD - 1 in a ring of registers (slot s % QG_RD, static
+  // after the unroll)
+  u32x4 wr[QG_RD][QG_NTW];
+  uint2 sr[QG_RD][QG_NTW];
   u32x4 xv[QG_XCH];
-  load_x(0, xv);
-  load_w(0, wr[0], sr[0]);
-  load_w(min(1, GP - 1), wr[1], sr[1]);
-  load_w(min(2, GP - 1), wr[2], sr[2]);
+  load_x(gq0, xv);
+#pragma unroll
+  for (int r = 0; r < QG_RD - 1; ++r) load_w(gq0 + min(r, NS - 1), wr[r], sr[r]);
   store_x(0, xv);
   lds_barrier();
-  for (int g0 = 0; g0 < GP; g0 += 4) {
+  for (int g0 = 0; g0 < NS; g0 += QG_RD) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int gp = g0 + u;
-      if (gp >= GP) break;  // uniform
-      const int buf = gp & 1;
+    for (int u = 0; u < QG_RD; ++u) {
+      const int gs = g0 + u;  // K-step of this range
+      if (gs >= NS) break;    // uniform
+      const int buf = gs & 1;
       // every load unconditional (the last steps re-read themselves), X first: the wait for
-      // X below then leaves the weights of step gp + 3 in flight
-      load_x(min(gp + 1, GP - 1), xv);
-      load_w(min(gp + 3, GP - 1), wr[(u + 3) & 3], sr[(u + 3) & 3]);
+      // X below then leaves the weights of step gp + QG_RD - 1 in flight
+      load_x(gq0 + min(gs + 1, NS - 1), xv);
+      load_w(gq0 + min(gs + QG_RD - 1, NS - 1), wr[(u + QG_RD - 1) % QG_RD], sr[(u + QG_RD - 1) % QG_RD]);
       const u32x4 (&wq0)[QG_NTW] = wr[u];
       const uint2 (&ws0)[QG_NTW] = sr[u];
-      // ---- compute K-step gp ----
+      // ---- compute K-step gs ----
       const uint16_t* xb = xl + (size_t)buf * MR * QG_XS;
       const float* sbuf = xsum + (size_t)buf * 2 * MR;
 #pragma unroll
@@ -774,8 +782,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
           }
         }
       }
-      if (gp + 1 < GP) store_x(buf ^ 1, xv);  // uniform
-      lds_barrier();  // step gp + 1 is in LDS; step gp's buffer is free for step gp + 2
+      if (gs + 1 < NS) store_x(buf ^ 1, xv);  // uniform
+      lds_barrier();  // step gs + 1 is in LDS; step gs's buffer is free for step gs + 2
     }
   }
   // ---- epilogues: this block's tokens m0 .. m0 + Mb - 1 ----
@@ -784,9 +792,64 @@ __global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
   e.y = a.y + (size_t)m0 * a.ldy;
   if (a.amax) e.amax = a.amax + (size_t)m0 * a.NT;
   if (a.ss_out) e.ss_out = a.ss_out + (size_t)m0 * a.ss_ld_out;
+  if (a.ksplit == 1) {
+#pragma unroll
+    for (int n = 0; n < QG_NTW; ++n)
+      if (tw + n < a.NT) epilogue<QG_MB>(e, acc[n], tw + n, c, r16);
+    return;
+  }
+  // split K: this token block's partials [ksplit][NT][MB][64][4] and counters [NT]
+  e.part = a.part + (size_t)blockIdx.y * a.ksplit * a.NT * QG_MB * 256;
+  e.counters = a.counters + (size_t)blockIdx.y * a.NT;
 #pragma unroll
   for (int n = 0; n < QG_NTW; ++n)
-    if (tw + n < a.NT) epilogue<QG_MB>(e, acc[n], tw + n, c, r16);
+    if (tw + n < a.NT) store_partial<QG_MB>(e, acc[n], tw + n, kq, lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int n = 0; n < QG_NTW; ++n)
+    if (tw + n < a.NT) arrive<QG_MB>(e, tw + n, lane, c, r16);
+}
+
+static int device_cus();
+
+// Split-K plan of the large-M GEMM: the K-range length (group pairs) and the number of
+// ranges that minimise the modelled time -- rounds of one block per CU times the steps per
+// block (plus about 1.5 steps of pipeline fill), plus the partials' HBM round trip priced
+// at 4 TB/s against a measured ~2.2 us per K-step of a block.  Depends on (NT, GP, the
+// token-block count, the CU count) only.
+void qgemm_plan(int NT, int GP, int M, int cus, int* kr, int* ksplit) {
+  const long tiles = (long)((NT + 4 * QG_NTW - 1) / (4 * QG_NTW)) * ((M + 16 * QG_MB - 1) / (16 * QG_MB));
+  double best = 0.0;
+  *kr = GP;
+  *ksplit = 1;
+  for (int ks = 1; ks <= QG_KSPLIT_MAX && ks <= GP; ++ks) {
+    const int r = (GP + ks - 1) / ks, kse = (GP + r - 1) / r;
+    if (kse != ks) continue;  // the same split as a smaller ks
+    const long blocks = tiles * kse;
+    const double rounds = (double)((blocks + cus - 1) / cus);
+    double us = rounds * (r + 1.5) * 2.2;
+    if (kse > 1) us += (double)blocks * 4 * QG_NTW * 16 * 16 * QG_MB * 4 * 2 / 4e6;
+    if (ks == 1 || us < best) {
+      best = us;
+      *kr = r;
+      *ksplit = kse;
+    }
+  }
+}
+
+void qgemm_workspace(int NT, int GP, int Mmax, size_t* part_floats, int* counters) {
+  const int cus = device_cus();
+  *part_floats = 0;
+  *counters = 0;
+  for (int mb = 1; mb <= (Mmax + 16 * QG_MB - 1) / (16 * QG_MB); ++mb) {
+    int kr, ks;
+    qgemm_plan(NT, GP, mb * 16 * QG_MB, cus, &kr, &ks);
+    if (ks > 1) {
+      *part_floats = std::max(*part_floats, (size_t)mb * ks * NT * QG_MB * 256);
+      *counters = std::max(*counters, mb * NT);
+    }
+  }
 }
 
 int qgemm_launch(const GemvArgs& a, hipStream_t st) {
@@ -795,8 +858,14 @@ int qgemm_launch(const GemvArgs& a, hipStream_t st) {
   if (a.norm_w) return fail(MC_E_INVALID, "qgemm: normalise the input rows first");
   if (a.amax && a.epi != EPI_STORE) return fail(MC_E_INVALID, "qgemm: argmax partials need the store epilogue");
   if (a.epi == EPI_RESIDUAL && a.N % 16) return fail(MC_E_INVALID, "qgemm: residual epilogue needs N % 16 == 0");
-  const dim3 grid((unsigned)((a.NT + 4 * QG_NTW - 1) / (4 * QG_NTW)), (unsigned)((a.M + 16 * QG_MB - 1) / (16 * QG_MB)));
-  hipLaunchKernelGGL(qgemm_kernel, grid, dim3(256), qgemm_lds_bytes(), st, a);
+  GemvArgs p = a;
+  qgemm_plan(a.NT, a.GP, a.M, device_cus(), &p.kr, &p.ksplit);
+  const unsigned mblocks = (unsigned)((a.M + 16 * QG_MB - 1) / (16 * QG_MB));
+  if (p.ksplit > 1 && (!a.part || a.part_floats < (size_t)mblocks * p.ksplit * a.NT * QG_MB * 256 || !a.counters ||
+                       (size_t)a.counters_n < (size_t)mblocks * a.NT))
+    return fail(MC_E_INVALID, "qgemm: split-K workspace too small");
+  const dim3 grid((unsigned)((a.NT + 4 * QG_NTW - 1) / (4 * QG_NTW)), mblocks, (unsigned)p.ksplit);
+  hipLaunchKernelGGL(qgemm_kernel, grid, dim3(256), qgemm_lds_bytes(), st, p);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
@@ -1146,7 +1215,7 @@ constexpr int MOE_ROUTE_PAIRS = 64 * 8;  // M <= 64 tokens x TK <= 8
 
 __global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, int M, int E, int TK, MoeRoute rt) {
   __shared__ int s_sel[MOE_ROUTE_PAIRS];
-  __shared__ int s_cnt[256], s_act[256], s_cum[256];
+  __shared__ int s_cnt[256], s_act[256];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int t = wave; t < M; t += 4) {
     float p[4];

@@ -83,6 +83,11 @@ int gemv_launch(const GemvArgs& a, int MT, hipStream_t st);
 // M > 64 tokens: every token tile of a block against each dequantised K-step (input rows
 // already normalised: norm_w must be NULL)
 int qgemm_launch(const GemvArgs& a, hipStream_t st);
+// Its split-K plan (group pairs per K-range, K-ranges) for M tokens on `cus` CUs, and the
+// workspace every M up to Mmax needs on the current device: partial floats and counters
+// (zero when no plan splits).
+void qgemm_plan(int NT, int GP, int M, int cus, int* kr, int* ksplit);
+void qgemm_workspace(int NT, int GP, int Mmax, size_t* part_floats, int* counters);
 int gemv_setup_lds();
 
 int qlinear_repack(const QLinear& L, int row_off, int row_stride, int Nsrc, const uint32_t* wq_dev,
