@@ -430,6 +430,7 @@ struct mc_batch {
   std::vector<int32_t> widths;
   std::vector<int32_t> kv_len_host;
   uint64_t unseeded = 0;
+  bool forced_none = true;  // the device's forced accept-length schedule is all -1
   // profiling
   bool profiling = false;
   std::vector<hipEvent_t> ev;
@@ -769,12 +770,15 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   size_t words = 0;
   auto take = [&](size_t n) { size_t o = words; words += (n + 1) & ~(size_t)1; return o; };  // 8-byte aligned in u32 units
   const size_t o_active = take(R), o_hist = take(R * b->hcap), o_hlen = take(R), o_gen = take(R), o_max = take(R),
-               o_cur = take(R), o_kv = take(R), o_temp = take(R), o_topp = take(R), o_invt = take(R),
+               o_cur = take(R), o_temp = take(R), o_topp = take(R), o_invt = take(R),
                o_hseed = take(R), o_seed = take(2 * R), o_ctr = take(2 * R), o_eos = take(8 * R), o_neos = take(R),
-               o_rej = take(R), o_dr = take(RK), o_np = take(R), o_stok = take(Ms), o_srow = take(Ms),
+               o_rej = take(R), o_dr = take(RK), o_stok = take(Ms), o_srow = take(Ms),
                o_spos = take(Ms), o_rs0 = take(R), o_nv = take(R), o_qb = take(R), o_sct = take(RK),
-               o_sca = take(RK), o_scr = take(RK), o_forced = take(R), o_otok = take(RK), o_ocnt = take(R),
-               o_ofin = take(R), o_stats = take(8);
+               o_sca = take(RK), o_scr = take(RK), o_forced = take(R), o_stats = take(8),
+               // what a step returns, contiguous so that one copy brings it to the host:
+               // [RK tokens | R counts | R finish | R proposal lengths | R KV lengths]
+               o_otok = take(RK + 4 * R), o_ocnt = o_otok + RK, o_ofin = o_ocnt + R, o_np = o_ofin + R,
+               o_kv = o_np + R;
   uint32_t* base;
   if ((rc = dev_zero(&base, words))) { batch_free(b); return rc; }
   b->scratch = base;
@@ -1367,11 +1371,13 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
   int rc;
   const int R = b->R, K1 = b->K1;
   // forced accept-length schedule (or none)
-  {
+  // (uploaded only when it differs from the all-none schedule already on the device)
+  if (forced_accept || !b->forced_none) {
     std::vector<int32_t> f((size_t)R, -1);
     if (forced_accept)
       for (int r = 0; r < R; ++r) f[(size_t)r] = forced_accept[r] < 0 ? -1 : forced_accept[r];
     if ((rc = upload_i32(b, b->s.forced, f.data(), (size_t)R))) return rc;
+    b->forced_none = forced_accept == nullptr;
   }
   // MC_STEP_EAGER=1 launches the step's kernels directly instead of replaying the captured
   // graph (same kernels; used under profilers that do not follow graph launches).
@@ -1406,11 +1412,8 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
   }
   const StepState& s = b->s;
   int32_t* h = b->h_out;
-  MC_HIP(hipMemcpyAsync(h, s.out_tok, (size_t)R * K1 * 4, hipMemcpyDeviceToHost, b->st));
-  MC_HIP(hipMemcpyAsync(h + R * K1, s.out_cnt, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
-  MC_HIP(hipMemcpyAsync(h + R * K1 + R, s.out_fin, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
-  MC_HIP(hipMemcpyAsync(h + R * K1 + 2 * R, s.nprop, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
-  MC_HIP(hipMemcpyAsync(h + R * K1 + 3 * R, s.kv_len, (size_t)R * 4, hipMemcpyDeviceToHost, b->st));
+  // tokens, counts, finish reasons, proposal and KV lengths sit contiguously on the device
+  MC_HIP(hipMemcpyAsync(h, s.out_tok, (size_t)(R * K1 + 4 * R) * 4, hipMemcpyDeviceToHost, b->st));
   h[R * K1 + 4 * R] = 0;
   if (b->fused_ok || b->xf_ok) MC_HIP(hipMemcpyAsync(h + R * K1 + 4 * R, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipStreamSynchronize(b->st));

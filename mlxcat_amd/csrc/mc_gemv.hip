@@ -903,8 +903,9 @@ void gemv_plan(const QLinear& L, int MT, int* kr, int* ksplit) {
     return;
   }
   const int Mr = 16;
-  // one K-range when it fits 5 group pairs per wave (no split-K tail), else 3 per wave
-  int d = (MT == 1 && L.GP <= GEMV_WAVES * 5) ? 5 : 3;
+  // one K-range when it fits 5 group pairs per wave (no split-K tail), else 4 per wave
+  // (K = 4096: two K-ranges, K = 9728: five; 4 per wave measured faster than 3 and 5)
+  int d = (MT == 1 && L.GP <= GEMV_WAVES * 5) ? 5 : 4;
   while (d > 1 && gemv_lds_bytes(Mr, GEMV_WAVES * d, MT) > (size_t)GEMV_LDS_LIMIT) --d;
   *kr = std::min(L.GP, GEMV_WAVES * d);
   *ksplit = (L.GP + *kr - 1) / *kr;
@@ -933,23 +934,17 @@ static void launch_mdu(const GemvArgs& a, size_t lds, hipStream_t st) {
 }
 
 // Units per block: enough that one round of resident blocks covers the launch (every
-// block stages its activations once, so fewer, longer-lived blocks amortise that).
+// block stages its activations once, so fewer, longer-lived blocks amortise that), but at
+// most 4: a block keeps only the next unit in flight, so longer queues (the vocab head
+// at 8 or 16 units per block) leave the weight stream latency-bound (head 110 -> 75 us).
 template <int MT, int D>
 static void launch_md(const GemvArgs& a, size_t lds, hipStream_t st) {
   const int nunits = a.NT * a.ksplit;
   const int cap = g_cus * occupancy<MT, D, 1>(lds);
   const int need = (nunits + cap - 1) / cap;
-  if (need <= 1) {
-    launch_mdu<MT, D, 1>(a, lds, st);
-  } else if (need == 2) {
-    launch_mdu<MT, D, 2>(a, lds, st);
-  } else if constexpr (MT > 1) {
-    launch_mdu<MT, D, 4>(a, lds, st);
-  } else {
-    if (need <= 4) launch_mdu<MT, D, 4>(a, lds, st);
-    else if (need <= 8) launch_mdu<MT, D, 8>(a, lds, st);
-    else launch_mdu<MT, D, 16>(a, lds, st);
-  }
+  if (need <= 1) launch_mdu<MT, D, 1>(a, lds, st);
+  else if (need == 2) launch_mdu<MT, D, 2>(a, lds, st);
+  else launch_mdu<MT, D, 4>(a, lds, st);
 }
 
 template <int MT>
@@ -1015,10 +1010,6 @@ static int setup_md() {
   const void* fns[] = {(const void*)qgemv_kernel<MT, D, 1>, (const void*)qgemv_kernel<MT, D, 2>,
                        (const void*)qgemv_kernel<MT, D, 4>};
   for (const void* f : fns) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
-  if constexpr (MT == 1) {
-    const void* more[] = {(const void*)qgemv_kernel<MT, D, 8>, (const void*)qgemv_kernel<MT, D, 16>};
-    for (const void* f : more) MC_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, GEMV_LDS_LIMIT));
-  }
   return MC_OK;
 }
 
