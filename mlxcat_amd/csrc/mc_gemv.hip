@@ -871,13 +871,17 @@ int qgemm_launch(const GemvArgs& a, hipStream_t st) {
 }
 
 // K-range plan of the multi-row classes: the largest K-range whose activations fit the LDS
-// cap (at most 8 group pairs), split further (down to 4 pairs) while the units cannot give
-// every wave of the device one.  Depends only on (N, K, MT) and the CU count.
+// cap (at most 8 group pairs), split further (down to 4 pairs) while there are fewer than
+// 4 units per CU.  Splitting until every wave of the device had a unit (8 per CU) cost
+// more in activation staging and partial sums than it gained in parallelism (batch-8
+// Qwen3-4B-shape step 5.50 -> 5.08 ms at 4 per CU).  Depends only on (N, K, MT) and the CU
+// count.
+constexpr int MID_UNITS_PER_CU = 4;
 void mid_plan(const QLinear& L, int MT, int cus, int* kr, int* ksplit) {
   int kmax = MID_KMAX;
   while (kmax > 1 && mid_lds_bytes(16 * MT, kmax, MT) > (size_t)MID_LDS_CAP) --kmax;
   int ks = (L.GP + kmax - 1) / kmax;
-  while ((size_t)L.NT * ks < (size_t)MID_WAVES * cus && (L.GP + ks) / (ks + 1) >= 4) ++ks;
+  while ((size_t)L.NT * ks < (size_t)MID_UNITS_PER_CU * cus && (L.GP + ks) / (ks + 1) >= 4) ++ks;
   *kr = (L.GP + ks - 1) / ks;
   *ksplit = (L.GP + *kr - 1) / *kr;
 }
