@@ -151,7 +151,8 @@ int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uin
 // ---------------------------------------------------------------------------
 // Split-KV attention, flash-decoding style, without LDS staging of K/V.  Grid
 // (R * nkv, splits); block (row, kv head, split) covers keys [split S 64, (split+1) S 64)
-// of the row, wave w its 64-key sub-chunks w, w + 4, ... (S >= 4).  K rows and V^T rows
+// of the row, wave w its 64-key sub-chunks w, w + 4, ... (S >= 2: at S < 4 some waves
+// have none and only join the merge).  K rows and V^T rows
 // go straight from the cache into MFMA operands:
 //   S^T[key][q] = K[key][:] . q[q][:]          v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 d,
 //                                              B = 32 d x 16 queries)
@@ -392,11 +393,13 @@ int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, i
   if (d != 64 && d != 128) return fail(MC_E_INVALID, "attention: head_dim must be 64 or 128");
   (void)max_q;
   const float scale = 1.0f / sqrtf((float)d);
-  // 64-key sub-chunks per block: at least two (two waves of a block take a chunk each
-  // and two wait: one decode row at 2K keys then spreads over twice the CUs that four
-  // would use, 10.0 -> 8.0 us per layer), more when the grid would exceed about 1024
-  // blocks (fewer partials to merge)
-  const int S = std::max(2, (R * nkv * w.nchunk + 1023) / 1024);
+  // 64-key sub-chunks per block: more when the grid would exceed about 1024 blocks (fewer
+  // partials to merge), and at least 2 (a few (row, kv head) pairs: one decode row spreads
+  // its 8 heads over more CUs, 10.0 -> 8.0 us per layer at 2K keys against 4) or 8 (64 or
+  // more pairs: two sub-chunks per wave, 4x fewer partials; batch 8 at 2K keys
+  // 5.08 -> 4.89 ms per step, 8 rows at 512-4096 keys 6.71 -> 6.28 ms).
+  const int smin = R * nkv >= 64 ? 8 : 2;
+  const int S = std::max(smin, (R * nkv * w.nchunk + 1023) / 1024);
   const dim3 grid(R * nkv, (w.nchunk + S - 1) / S);
   if (d == 128) hipLaunchKernelGGL(attn_flash_kernel<128>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
   else hipLaunchKernelGGL(attn_flash_kernel<64>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
