@@ -215,15 +215,35 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int k2 = 0; k2 < a.ksplit; ++k2) {
+  // the partials of KB K-ranges are loaded together (one memory round trip per KB ranges,
+  // not per range: the tail of a launch is its last tile's reduction), then summed in
+  // K-range order; ranges past the last are neither loaded nor summed
+  constexpr int KB = MT == 1 ? 8 : 4;
+  for (int k0 = 0; k0 < a.ksplit; k0 += KB) {
+    float2 p[KB][MT][2];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float* src = a.part + ((((size_t)k2 * a.NT + t) * MT + mt) * 64 + lane) * 4;
-      const float2 p0 = ld_coherent(src), p1 = ld_coherent(src + 2);
-      acc[mt][0] += p0.x;
-      acc[mt][1] += p0.y;
-      acc[mt][2] += p1.x;
-      acc[mt][3] += p1.y;
+    for (int j = 0; j < KB; ++j) {
+      const int k2 = k0 + j;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float* src = a.part + ((((size_t)k2 * a.NT + t) * MT + mt) * 64 + lane) * 4;
+        p[j][mt][0] = p[j][mt][1] = make_float2(0.f, 0.f);
+        if (k2 < a.ksplit) {
+          p[j][mt][0] = ld_coherent(src);
+          p[j][mt][1] = ld_coherent(src + 2);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (k0 + j >= a.ksplit) break;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] += p[j][mt][0].x;
+        acc[mt][1] += p[j][mt][0].y;
+        acc[mt][2] += p[j][mt][1].x;
+        acc[mt][3] += p[j][mt][1].y;
+      }
     }
   }
   if (lane == 0) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
