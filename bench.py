@@ -9,8 +9,8 @@ positions copied from earlier spans.  A step is one speculative step (n-gram pro
 the timed region.  The same workload at batch 8 is reported beside it.
 
 Prints one JSON line: accepted tokens/s at batch 1 (value), the batch-8 figure, the
-verify-step latency, the live HBM roofline of the dominant kernel (the dequant GEMV, or
-the persistent forward kernel when the step runs it; timed with HIP events on its stream),
+verify-step latency, the live HBM roofline of the dominant kernel (the dequant GEMV, timed
+with HIP events on its stream),
 its measured HBM traffic per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, recorded in
 profiles/), and the CPU oracle timed on a bounded sample.
 """
@@ -63,7 +63,7 @@ def step_bytes(cfg: dict, ctx_lens, M: int) -> float:
     return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
 
 
-def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forward_mode: int = 1):
+def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
     from mlxcat_amd import _lib as hip
     from mlxcat_amd.workloads import copy_span_prompt
     L = hip.load()
@@ -74,7 +74,6 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forward_mode: int
     max_new = (warmup + steps + 8) * (K_DRAFT + 1) + 8
     ctx = PROMPT_LEN + max_new + K_DRAFT + 16
     b = hip.Batch(m, rows, ctx, spec_cfg(rows))
-    b.set_fused(forward_mode)
     for r in range(rows):
         p = copy_span_prompt(SEED + r, PROMPT_LEN, QWEN3_4B["vocab"])
         b.insert(r, p, max_new, hip.make_sampling())
@@ -95,20 +94,17 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forward_mode: int
                bytes_per_step=step_bytes(QWEN3_4B, kv0, rows * (K_DRAFT + 1)))
     out["step_hbm_gbs"] = out["bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
     if profile:
-        # kind 3: the persistent forward (one launch per step); kind 0: the dequant GEMVs
+        # kind 0: the dequant GEMVs of the verify forward, timed with HIP events on the batch stream
         b.set_profiling(True)
-        acc = {k: [0.0, 0.0, 0] for k in (0, 3)}
+        acc = [0.0, 0.0, 0]
         for _ in range(3):
             b.step()
-            for k in (0, 3):
-                ms, by, n = b.profile(k)
-                acc[k][0] += ms
-                acc[k][1] += by
-                acc[k][2] += n
+            ms, by, n = b.profile(0)
+            acc[0] += ms
+            acc[1] += by
+            acc[2] += n
         b.set_profiling(False)
-        k = 3 if acc[3][2] > 0 else 0
-        out["dominant"] = dict(ms=acc[k][0] / 3, bytes=acc[k][1] / 3, launches=acc[k][2] // 3,
-                               kernel="fused_forward_kernel" if k == 3 else "qgemv_kernel<1>")
+        out["dominant"] = dict(ms=acc[0] / 3, bytes=acc[1] / 3, launches=acc[2] // 3, kernel="qgemv_kernel<1>")
     b.close()
     m.close()
     return out
@@ -155,7 +151,6 @@ def run_config(name: str, steps: int, warmup: int) -> dict:
     spec = dict(enabled=1, max_proposal_tokens=k, max_suffix_tokens=MATCH, min_context_tokens=8, acceptance=1,
                 single_row_only=0, greedy_only=0)
     b = hip.Batch(m, rows, max(lens) + max_new + k + 16, spec)
-    b.set_fused(0)
     for r in range(rows):
         if samp == "greedy" or (samp == "even-greedy-odd-seeded" and r % 2 == 0):
             sp = hip.make_sampling()
@@ -223,9 +218,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
-    ap.add_argument("--forward", choices=["multi", "persistent", "auto"], default="multi",
-                    help="verify forward: the per-layer kernels (the faster path on MI355X today), the persistent "
-                         "forward kernel (required), or the persistent kernel whenever the shape allows it")
     ap.add_argument("--config", choices=sorted(CONFIGS), default=None,
                     help="measure one of the other workloads instead (its own JSON line)")
     ap.add_argument("--copy-ref", action="store_true",
@@ -241,7 +233,6 @@ def main():
         torch.cuda.synchronize()
         print("copied 3 x 256 MiB", flush=True)
         return
-    mode = {"auto": 1, "persistent": 2, "multi": 0}[a.forward]
     if a.config:
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
@@ -254,9 +245,8 @@ def main():
         print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
-    b1 = run_gpu(1, a.steps, a.warmup, profile=True, forward_mode=mode)
-    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False,
-                                      forward_mode=0 if mode == 0 else 1)
+    b1 = run_gpu(1, a.steps, a.warmup, profile=True)
+    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False)
     cpu = None if a.no_cpu else run_cpu()
     g = b1["dominant"]
     achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9

@@ -210,20 +210,10 @@ int mc_batch_stats(mc_batch* b, mc_spec_stats* out);
  * accounting, SchedulerSpeculativeDecodingTests.swift:202-208); returns the count. */
 int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap);
 
-/* ---- forward implementation ----
- * No counterpart in the reference (its forward is MLX's).  Forwards of at most 8 tokens
- * over a batch of at most 8 rows can run as one persistent kernel (mc_fused.hip) instead
- * of ~7 kernels per layer.  mode: 0 = never, 1 = whenever the call allows (default),
- * 2 = required (calls it cannot serve fail with MC_E_STATE).  Tests use it to check both
- * forwards against the oracle. */
-int mc_batch_set_fused(mc_batch* b, int32_t mode);
-/* 1 when the model and batch shape allow the persistent forward, else 0. */
-int mc_batch_fused_available(mc_batch* b);
-
 /* ---- timing support ---- */
 /* Average device time (ms) of each kernel class over the last mc_step when profiling is
  * enabled; used by bench.py for the live roofline.  kind: 0 = dequant GEMV (all),
- * 1 = attention, 2 = whole verify step, 3 = persistent forward. */
+ * 1 = attention, 2 = whole verify step. */
 int mc_batch_set_profiling(mc_batch* b, int32_t enabled);
 int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches);
 

@@ -27,7 +27,7 @@ EXPORTS = [
     "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
     "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_history",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
-    "mc_batch_set_profiling", "mc_batch_profile", "mc_batch_set_fused", "mc_batch_fused_available",
+    "mc_batch_set_profiling", "mc_batch_profile",
 ]
 
 
@@ -107,8 +107,6 @@ def load(path: str = LIB_PATH):
         "mc_batch_call_widths": (C.c_int, [P, P, I32]),
         "mc_batch_set_profiling": (C.c_int, [P, I32]),
         "mc_batch_profile": (C.c_int, [P, I32, P, P, P]),
-        "mc_batch_set_fused": (C.c_int, [P, I32]),
-        "mc_batch_fused_available": (C.c_int, [P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -296,14 +294,6 @@ class Batch:
 
     def set_profiling(self, enabled: bool) -> None:
         _check(load().mc_batch_set_profiling(self.h, 1 if enabled else 0))
-
-    def set_fused(self, mode: int) -> None:
-        """Forward implementation: 0 = multi-kernel, 1 = persistent kernel when the call
-        allows (default), 2 = persistent kernel required."""
-        _check(load().mc_batch_set_fused(self.h, mode))
-
-    def fused_available(self) -> bool:
-        return bool(load().mc_batch_fused_available(self.h))
 
     def profile(self, kind: int):
         ms, by, n = C.c_double(), C.c_double(), C.c_int32()

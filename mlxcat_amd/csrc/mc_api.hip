@@ -10,11 +10,9 @@
 #include <string>
 #include <vector>
 
-#include "mc_fused.hpp"
 #include "mc_gemv.hpp"
 #include "mc_kernels.hpp"
 #include "mc_step.hpp"
-#include "mc_xfwd.hpp"
 
 namespace mc {
 
@@ -424,7 +422,7 @@ struct mc_batch {
   // pinned staging
   int32_t* h_i32 = nullptr;  // general staging
   size_t h_i32_n = 0;
-  int32_t* h_out = nullptr;  // [R*K1 tok | R cnt | R fin | R nprop | R kv_len | persistent-forward error]
+  int32_t* h_out = nullptr;  // [R*K1 tok | R cnt | R fin | R nprop | R kv_len]
   hipGraphExec_t graph = nullptr;
   hipGraph_t graph_def = nullptr;
   std::vector<int32_t> widths;
@@ -437,23 +435,8 @@ struct mc_batch {
   size_t ev_used = 0;
   struct Rec { int kind; size_t e0, e1; double bytes; };
   std::vector<Rec> recs;
-  double prof_ms[4] = {0, 0, 0, 0}, prof_bytes[4] = {0, 0, 0, 0};
-  int prof_launch[4] = {0, 0, 0, 0};
-  // persistent forward (mc_fused): at most FW_MMAX tokens over at most FW_MMAX rows
-  int fused_mode = 1;            // 0 off, 1 whenever the call allows it, 2 required
-  bool fused_ok = false;         // model and batch shape supported
-  FwArgs fw{};                   // fixed arguments; M and the logits flag are set per call
-  FwLayer* fw_layers = nullptr;  // device [n_layers]
-  unsigned long long* fw_ll = nullptr;
-  unsigned* fw_ctl = nullptr;    // [0] forward-call counter (starts at 1), [1] error word, [8..15] XCD arrivals
-  int fw_grid = 0;
-  // XCD-partitioned persistent forward (mc_xfwd): preferred when available
-  bool xf_ok = false;
-  XArgs xf{};
-  XArgs* xf_args = nullptr;      // device copy of xf
-  XLayer* xf_layers = nullptr;   // device [n_layers]
-  unsigned long long* xf_ll = nullptr;
-  int xf_grid = 0;
+  double prof_ms[3] = {0, 0, 0}, prof_bytes[3] = {0, 0, 0};
+  int prof_launch[3] = {0, 0, 0};
 };
 
 static void batch_free(mc_batch* b) {
@@ -464,7 +447,6 @@ static void batch_free(mc_batch* b) {
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
                   (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
-                  (void*)b->fw_layers, (void*)b->fw_ll, (void*)b->fw_ctl, (void*)b->xf_layers, (void*)b->xf_ll, (void*)b->xf_args,
                   (void*)b->moe_xn, (void*)b->moe_logits, (void*)b->moe_act, (void*)b->moe_out, (void*)b->moe_i32,
                   (void*)b->moe_wts, (void*)b->xn})
     if (p) (void)hipFree(p);
@@ -483,174 +465,6 @@ static int stage_i32(mc_batch* b, size_t n) {
   b->h_i32 = nullptr;
   MC_HIP(hipHostMalloc((void**)&b->h_i32, n * 4, hipHostMallocDefault));
   b->h_i32_n = n;
-  return MC_OK;
-}
-
-// Control words shared by the persistent forwards: call counter (starts at 1), error word,
-// per-XCD arrival counters.
-static int ctl_setup(mc_batch* b) {
-  int rc;
-  if ((rc = dev_zero(&b->fw_ctl, 16))) return rc;
-  const unsigned one = 1u;
-  MC_HIP(hipMemcpy(b->fw_ctl, &one, 4, hipMemcpyHostToDevice));
-  return MC_OK;
-}
-
-static XLin xlin(const QLinear& L) {
-  XLin x;
-  x.qw = L.qw; x.sb = L.sb; x.N = L.N; x.K = L.K; x.NT = L.NT; x.GP = L.GP;
-  return x;
-}
-
-// XCD-partitioned persistent forward (mc_xfwd), when the model, the batch and the device
-// allow it.  Not an error otherwise.
-static int xfwd_setup(mc_batch* b, int kcap) {
-  mc_model* m = b->m;
-  const auto& c = m->cfg;
-  int cus = 0;
-  MC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device));
-  const char* why = nullptr;
-  if (!xfwd_supported(c, b->R, kcap, cus, &why)) return MC_OK;
-  XArgs& a = b->xf;
-  a.bpx = cus / XF_XCD;
-  if (a.bpx & (a.bpx - 1)) return MC_OK;  // the norm reduction pairs lanes by powers of two
-  a.L = c.n_layers;
-  a.H = c.hidden; a.nq = c.n_q_heads; a.nkv = c.n_kv_heads; a.d = c.head_dim; a.I = c.intermediate; a.V = c.vocab;
-  a.eps = c.rms_eps;
-  a.scale = 1.0f / sqrtf((float)a.d);
-  if (!xfwd_plan(a)) return MC_OK;
-  std::vector<XLayer> hl((size_t)c.n_layers);
-  for (int l = 0; l < c.n_layers; ++l) {
-    const auto& L = m->layers[(size_t)l];
-    XLayer& f = hl[(size_t)l];
-    f.qkv = xlin(L.qkv); f.o = xlin(L.o); f.gu = xlin(L.gateup); f.dn = xlin(L.down);
-    f.in_norm = L.in_norm; f.post_norm = L.post_norm; f.q_norm = L.q_norm; f.k_norm = L.k_norm;
-    f.k = b->kv[(size_t)l].k;
-    f.v = b->kv[(size_t)l].v;
-  }
-  int rc;
-  if ((rc = dev_alloc(&b->xf_layers, hl.size()))) return rc;
-  MC_HIP(hipMemcpy(b->xf_layers, hl.data(), hl.size() * sizeof(XLayer), hipMemcpyHostToDevice));
-  const size_t mm = XF_MMAX, X8 = XF_XCD, g = (size_t)(a.nq / a.nkv);
-  a.nch_cap = kcap / 64;
-  const size_t n_x = X8 * mm * a.H / 2, n_ss = X8 * a.bpx * mm, n_qkv = X8 * mm * (g + 2) * a.d / 2,
-               n_rec = X8 * b->R * a.nch_cap * 32 * XF_REC, n_att = X8 * mm * g * a.d / 2, n_part = X8 * mm * a.H,
-               n_act = X8 * mm * a.act_w;
-  if ((rc = dev_zero(&b->xf_ll, 2 * n_x + 2 * n_ss + n_qkv + n_rec + n_att + 2 * n_part + n_act))) return rc;
-  unsigned long long* p = b->xf_ll;
-  a.xl = p; p += n_x;
-  a.x1l = p; p += n_x;
-  a.xss = p; p += n_ss;
-  a.x1ss = p; p += n_ss;
-  a.qkvl = p; p += n_qkv;
-  a.rec = p; p += n_rec;
-  a.attl = p; p += n_att;
-  a.opart = p; p += n_part;
-  a.dpart = p; p += n_part;
-  a.actl = p;
-  a.layers = b->xf_layers;
-  a.embed = xlin(m->embed);
-  a.head = xlin(m->head());
-  a.final_norm = m->final_norm;
-  a.rope_cos = b->rope_cos;
-  a.rope_sin = b->rope_sin;
-  a.cap = kcap;
-  a.R = b->R;
-  a.epoch = b->fw_ctl;
-  a.err = b->fw_ctl + 1;
-  a.xcd_ctr = b->fw_ctl + 8;
-  b->xf_grid = cus;
-  b->xf_ok = true;
-  return MC_OK;
-}
-
-// The XCD-partitioned forward's arguments into device memory, once the step state (slot
-// arrays) and the logits buffer exist.
-static int xfwd_finish(mc_batch* b) {
-  if (!b->xf_ok) return MC_OK;
-  XArgs& a = b->xf;
-  a.slot_tok = b->s.slot_tok;
-  a.slot_row = b->s.slot_row;
-  a.row_slot0 = b->s.row_slot0;
-  a.n_valid = b->s.n_valid;
-  a.qbase = b->s.qbase;
-  a.logits = b->logits;
-  a.amax = b->amax;
-  int rc;
-  if ((rc = dev_alloc(&b->xf_args, 1))) return rc;
-  MC_HIP(hipMemcpy(b->xf_args, &a, sizeof(XArgs), hipMemcpyHostToDevice));
-  return MC_OK;
-}
-
-// Persistent-forward resources, when the model and the batch allow them (at most FW_MMAX
-// rows).  Not an error otherwise: the multi-kernel forward serves every call.
-static int fused_setup(mc_batch* b, int kcap) {
-  mc_model* m = b->m;
-  const auto& c = m->cfg;
-  const char* why = nullptr;
-  if (b->R > FW_MMAX || !fused_supported(c, 1, kcap, &why)) return MC_OK;
-  const int grid = fused_grid(m->device);
-  if (grid < 1) return MC_OK;
-  std::vector<FwLayer> hl((size_t)c.n_layers);
-  int oks = 1, dks = 1;
-  for (int l = 0; l < c.n_layers; ++l) {
-    const auto& L = m->layers[(size_t)l];
-    FwLayer& f = hl[(size_t)l];
-    f.qkv = fused_lin(L.qkv, 1);
-    f.o = fused_lin(L.o, 4);
-    f.gu = fused_lin(L.gateup, 1);
-    f.dn = fused_lin(L.down, 4);
-    if (!f.qkv.ks || !f.o.ks || !f.gu.ks || !f.dn.ks) return MC_OK;
-    oks = std::max(oks, f.o.ks);
-    dks = std::max(dks, f.dn.ks);
-    f.in_norm = L.in_norm;
-    f.post_norm = L.post_norm;
-    f.q_norm = L.q_norm;
-    f.k_norm = L.k_norm;
-    f.k = b->kv[(size_t)l].k;
-    f.v = b->kv[(size_t)l].v;
-  }
-  const FwLin head = fused_lin(m->head(), 1);
-  if (!head.ks) return MC_OK;
-  int rc;
-  if ((rc = dev_alloc(&b->fw_layers, hl.size()))) return rc;
-  MC_HIP(hipMemcpy(b->fw_layers, hl.data(), hl.size() * sizeof(FwLayer), hipMemcpyHostToDevice));
-  const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
-  const size_t Nqkv = (size_t)(nq + 2 * nkv) * d;
-  const int npb = fused_npb_cap(kcap);
-  const size_t mm = FW_MMAX;
-  const size_t n_x = mm * H / 2, n_xss = mm * H / 16, n_qkv = mm * Nqkv / 2, n_att = mm * nq * d / 2,
-               n_act = mm * I / 2, n_op = (size_t)oks * mm * H, n_dp = (size_t)dks * mm * H,
-               n_ao = (size_t)b->R * nkv * npb * FW_QROWS * d, n_aml = (size_t)b->R * nkv * npb * FW_QROWS * 2;
-  if ((rc = dev_zero(&b->fw_ll, n_x + n_xss + n_qkv + n_att + n_act + n_op + n_dp + n_ao + n_aml))) return rc;
-  FwArgs& a = b->fw;
-  unsigned long long* p = b->fw_ll;
-  a.x = p; p += n_x;
-  a.xss = p; p += n_xss;
-  a.qkv = p; p += n_qkv;
-  a.att = p; p += n_att;
-  a.act = p; p += n_act;
-  a.opart = p; p += n_op;
-  a.dpart = p; p += n_dp;
-  a.ao = p; p += n_ao;
-  a.aml = p;
-  a.npb_cap = npb;
-  a.layers = b->fw_layers;
-  a.L = c.n_layers;
-  a.embed = m->embed;
-  a.head = head;
-  a.final_norm = m->final_norm;
-  a.H = H; a.nq = nq; a.nkv = nkv; a.d = d; a.I = I; a.V = c.vocab;
-  a.eps = c.rms_eps;
-  a.scale = 1.0f / sqrtf((float)d);
-  a.rope_cos = b->rope_cos;
-  a.rope_sin = b->rope_sin;
-  a.cap = kcap;
-  a.R = b->R;
-  a.epoch = b->fw_ctl;
-  a.err = b->fw_ctl + 1;
-  b->fw_grid = grid;
-  b->fused_ok = true;
   return MC_OK;
 }
 
@@ -757,7 +571,6 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
         return rc;
       }
     }
-    if ((rc = ctl_setup(b)) || (rc = fused_setup(b, kcap)) || (rc = xfwd_setup(b, kcap))) { batch_free(b); return rc; }
   }
   if ((rc = dev_zero(&b->logits, (size_t)M * V))) { batch_free(b); return rc; }
 
@@ -801,8 +614,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     MC_HIP(hipMemcpy(s.reject, neg.data(), R * 4, hipMemcpyHostToDevice));
   }
   if ((rc = stage_i32(b, std::max<size_t>(4096, (size_t)b->hcap + 16)))) { batch_free(b); return rc; }
-  MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R + 1) * 4, hipHostMallocDefault));
-  if ((rc = xfwd_finish(b))) { batch_free(b); return rc; }
+  MC_HIP(hipHostMalloc((void**)&b->h_out, (RK + 4 * R) * 4, hipHostMallocDefault));
   *out = b;
   return MC_OK;
 }
@@ -829,25 +641,6 @@ static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
   return MC_OK;
 }
 
-// The persistent forward over the M slots described in the StepState arrays (all rows of
-// the batch, at most FW_MMAX), logits for every slot when with_logits.
-static int fused_forward(mc_batch* b, int M, bool with_logits) {
-  FwArgs a = b->fw;
-  const StepState& s = b->s;
-  a.M = M;
-  a.with_head = with_logits ? 1 : 0;
-  a.slot_tok = s.slot_tok;
-  a.slot_row = s.slot_row;
-  a.row_slot0 = s.row_slot0;
-  a.n_valid = s.n_valid;
-  a.qbase = s.qbase;
-  a.logits = b->logits;
-  a.amax = b->amax;
-  int rc = launch_fused_forward(a, b->fw_grid, b->st);
-  if (rc) return rc;
-  return launch_epoch_bump(b->fw_ctl, b->st);
-}
-
 // Algorithmic HBM bytes of one forward over M slots: every linear's packed weights
 // (0.5625 B per weight), the cached K/V read, the new K/V written, the bf16 logits.
 static double forward_alg_bytes(const mc_batch* b, int M, bool with_head) {
@@ -860,25 +653,6 @@ static double forward_alg_bytes(const mc_batch* b, int M, bool with_head) {
   for (int r = 0; r < b->R; ++r) ctx += b->kv_len_host[(size_t)r];
   const double kv_row = (double)c.n_layers * 2 * c.n_kv_heads * c.head_dim * 2;
   return w + ctx * kv_row + (double)M * kv_row;
-}
-
-// Whether this forward runs as a persistent kernel (the XCD-partitioned one first).
-static bool use_xf(const mc_batch* b, int M) { return b->xf_ok && b->fused_mode != 0 && M >= 1 && M <= XF_MMAX; }
-static bool use_fused(const mc_batch* b, int M) { return b->fused_ok && b->fused_mode != 0 && M >= 1 && M <= FW_MMAX; }
-
-static int xf_forward(mc_batch* b, int M, bool with_logits) {
-  int rc = launch_xfwd(b->xf_args, b->xf.lds_bytes, M, with_logits ? 1 : 0, b->xf_grid, b->st);
-  if (rc) return rc;
-  return launch_xfwd_epoch(b->fw_ctl, b->fw_ctl + 8, b->st);
-}
-
-// The persistent forward's error word (nonzero: a wait timed out or the unit schedule broke).
-static int fused_check(mc_batch* b) {
-  if (!b->fused_ok && !b->xf_ok) return MC_OK;
-  unsigned e = 0;
-  MC_HIP(hipMemcpy(&e, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost));
-  if (e) return fail(MC_E_STATE, e & 4u ? "persistent forward: XCD placement" : e & 2u ? "persistent forward: unit schedule mismatch" : "persistent forward: wait timed out");
-  return MC_OK;
 }
 
 // One linear over M tokens, in launches of at most 64.  norm_w: the input rows are the
@@ -1013,21 +787,6 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
     if (lgn > 0) return launch_fake_logits(c.arch, s.slot_tok + lg0, lgn, c.vocab, b->logits + (size_t)lg0 * c.vocab, b->st);
     return MC_OK;
   }
-  if (use_xf(b, M)) {
-    size_t e0 = 0;
-    if ((rc = prof_begin(b, &e0))) return rc;
-    if ((rc = xf_forward(b, M, lgn > 0))) return rc;
-    if ((rc = prof_end(b, e0, 3, forward_alg_bytes(b, M, lgn > 0)))) return rc;
-    return MC_OK;
-  }
-  if (use_fused(b, M)) {
-    size_t e0 = 0;
-    if ((rc = prof_begin(b, &e0))) return rc;
-    if ((rc = fused_forward(b, M, lgn > 0))) return rc;
-    if ((rc = prof_end(b, e0, 3, forward_alg_bytes(b, M, lgn > 0)))) return rc;
-    return MC_OK;
-  }
-  if (b->fused_mode == 2) return fail(MC_E_STATE, "persistent forward required but not available for this call");
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
@@ -1137,7 +896,7 @@ extern "C" int mc_forward(mc_batch* b, int32_t nrows, const int32_t* rows, const
     MC_HIP(hipMemcpyAsync(logits_host, b->logits, (size_t)M * b->m->cfg.vocab * 2, hipMemcpyDeviceToHost, b->st));
   }
   MC_HIP(hipStreamSynchronize(b->st));
-  return fused_check(b);
+  return MC_OK;
 }
 
 // --------------------------- admission ------------------------------------
@@ -1414,15 +1173,7 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
   int32_t* h = b->h_out;
   // tokens, counts, finish reasons, proposal and KV lengths sit contiguously on the device
   MC_HIP(hipMemcpyAsync(h, s.out_tok, (size_t)(R * K1 + 4 * R) * 4, hipMemcpyDeviceToHost, b->st));
-  h[R * K1 + 4 * R] = 0;
-  if (b->fused_ok || b->xf_ok) MC_HIP(hipMemcpyAsync(h + R * K1 + 4 * R, b->fw_ctl + 1, 4, hipMemcpyDeviceToHost, b->st));
   MC_HIP(hipStreamSynchronize(b->st));
-  if (h[R * K1 + 4 * R]) {
-    const unsigned e = (unsigned)h[R * K1 + 4 * R];
-    return fail(MC_E_STATE, e & 4u   ? "persistent forward: XCD placement"
-                            : e & 2u ? "persistent forward: unit schedule mismatch"
-                                     : "persistent forward: wait timed out");
-  }
   if (out_tokens) memcpy(out_tokens, h, (size_t)R * K1 * 4);
   if (out_counts) memcpy(out_counts, h + R * K1, (size_t)R * 4);
   if (out_finish) memcpy(out_finish, h + R * K1 + R, (size_t)R * 4);
@@ -1431,7 +1182,7 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_t
     b->kv_len_host[(size_t)r] = h[R * K1 + 3 * R + r];
   }
   if (b->profiling) {
-    for (int k = 0; k < 4; ++k) { b->prof_ms[k] = 0; b->prof_bytes[k] = 0; b->prof_launch[k] = 0; }
+    for (int k = 0; k < 3; ++k) { b->prof_ms[k] = 0; b->prof_bytes[k] = 0; b->prof_launch[k] = 0; }
     for (const auto& rec : b->recs) {
       float ms = 0;
       MC_HIP(hipEventElapsedTime(&ms, b->ev[rec.e0], b->ev[rec.e1]));
@@ -1463,21 +1214,6 @@ extern "C" int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap) {
   return n;
 }
 
-extern "C" int mc_batch_set_fused(mc_batch* b, int32_t mode) {
-  if (!b || mode < 0 || mode > 2) return fail(MC_E_INVALID, "mc_batch_set_fused: bad argument");
-  if (mode == 2 && !b->fused_ok && !b->xf_ok) return fail(MC_E_STATE, "persistent forward not available for this model / batch");
-  b->fused_mode = mode;
-  if (b->graph) {  // the captured step follows the mode it was captured with
-    MC_HIP(hipGraphExecDestroy(b->graph));
-    b->graph = nullptr;
-    if (b->graph_def) MC_HIP(hipGraphDestroy(b->graph_def));
-    b->graph_def = nullptr;
-  }
-  return MC_OK;
-}
-
-extern "C" int mc_batch_fused_available(mc_batch* b) { return b && (b->fused_ok || b->xf_ok) ? 1 : 0; }
-
 extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
   if (!b) return fail(MC_E_INVALID, "null batch");
   b->profiling = enabled != 0;
@@ -1485,7 +1221,7 @@ extern "C" int mc_batch_set_profiling(mc_batch* b, int32_t enabled) {
 }
 
 extern "C" int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches) {
-  if (!b || kind < 0 || kind > 3) return fail(MC_E_INVALID, "bad argument");
+  if (!b || kind < 0 || kind > 2) return fail(MC_E_INVALID, "bad argument");
   if (ms) *ms = b->prof_ms[kind];
   if (bytes) *bytes = b->prof_bytes[kind];
   if (launches) *launches = b->prof_launch[kind];

@@ -2,25 +2,23 @@
 // mlxcat_amd/csrc compiled as host C++), checked against the oracle.  Test infrastructure.
 //
 // usage: lib_emu <case>
-//   case 0: small head_dim-128 model; 40-token prefill (multi-kernel forward), then verify
-//           blocks of 6, 1 and 8 tokens with the persistent forward required; logits and
-//           the whole K/V against the oracle
-//   case 1: the same model and prefill, verify blocks with the multi-kernel forward
-//   case 2: Qwen3-4B shape (2 layers): 40-token prefill, a 6-token verify (persistent)
-//   case 3: case 0 with 32 q / 8 kv heads, hidden 512 (the XCD-partitioned forward; EMU_CUS=32)
+//   case 0: small head_dim-128 model; 40-token prefill, then verify blocks of 6, 1 and 8
+//           tokens; logits and the whole K/V against the oracle
+//   case 1: the same as case 0 (kept for the numbering of older notes)
+//   case 2: Qwen3-4B shape (2 layers): 40-token prefill, a 6-token verify
+//   case 3: case 0 with 32 q / 8 kv heads, hidden 512 (GQA group 4, eight kv heads)
 //   case 4: the case-3 model through mc_step (verify blocks with padding slots; MC_STEP_EAGER=1)
-//   case 5: a small Qwen3-MoE model (16 experts, top-4) through the multi-kernel forward
+//   case 5: a small Qwen3-MoE model (16 experts, top-4)
 //   case 6: the case-0 model, 12 rows: one verify block of 12 x 6 = 72 tokens (the M > 64 GEMM)
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <vector>
 
 #include "../../include/mlxcat_hip.h"
-#include "../../mlxcat_amd/csrc/mc_fused.hpp"
-#include "../../mlxcat_amd/csrc/mc_xfwd.hpp"
 #include "emu.hpp"
 
 extern "C" {
@@ -59,8 +57,6 @@ static void compare(const char* what, const uint16_t* got, const uint16_t* want,
 int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
-  emu::set_persistent((const void*)mc::fused_forward_kernel);
-  emu::set_persistent((const void*)mc::xfwd_kernel);
   check(mc_set_device(0), "set_device");
   mc_model_config c{};
   c.arch = 0; c.n_layers = 2; c.hidden = 256; c.n_q_heads = 4; c.n_kv_heads = 2; c.head_dim = 128;
@@ -68,10 +64,10 @@ int main(int argc, char** argv) {
   if (cs == 2) {
     c.hidden = 2560; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 9728; c.vocab = 151936;
   }
-  if (cs == 3) {  // smallest shape of the XCD-partitioned forward: 8 kv heads, GQA group 4
+  if (cs == 3) {  // 8 kv heads, GQA group 4
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
-  if (cs == 4) {  // speculative steps through the XCD-partitioned forward: padding slots
+  if (cs == 4) {  // speculative steps: padding slots
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
   if (cs == 5) {  // Qwen3-MoE: 16 experts of width 128, top-4 (a 40-token prefill gives experts > 16 pairs)
@@ -85,10 +81,9 @@ int main(int argc, char** argv) {
   mc_spec_config spec{1, 5, 3, 8, 1, 0, 0};
   mc_batch* b = nullptr;
   check(mc_batch_create(m, 1, ctx, 5, &spec, &b), "batch_create");
-  printf("persistent forward available: %d\n", mc_batch_fused_available(b));
   if (cs == 4) {
     // a prompt without repeats (no drafts: one valid slot of six) and a repeating one
-    // (drafts), each stepped with the persistent forward and with the multi-kernel forward
+    // (drafts), each stepped twice from a fresh batch (the two runs must agree)
     std::vector<std::vector<int32_t>> outs;
     for (int pass = 0; pass < 4; ++pass) {
       mc_batch* bb = nullptr;
@@ -99,7 +94,6 @@ int main(int argc, char** argv) {
       sp.reject_token = -1;
       int32_t first = 0, fin = 0;
       check(mc_batch_insert(bb, 0, prompt.data(), 48, 24, &sp, &first, &fin), "insert");
-      check(mc_batch_set_fused(bb, pass & 1 ? 0 : 2), "set_fused");  // the prefill took the multi-kernel forward
       std::vector<int32_t> toks{first};
       for (int st = 0; st < 6; ++st) {
         int32_t ot[6], cnt[1], f[1];
@@ -107,14 +101,13 @@ int main(int argc, char** argv) {
         for (int k = 0; k < cnt[0]; ++k) toks.push_back(ot[k]);
         if (cnt[0] == 0) break;
       }
-      printf("pass %d (%s, %s): %zu tokens:", pass, pass < 2 ? "no repeats" : "repeats", pass & 1 ? "multi" : "persistent",
-             toks.size());
+      printf("pass %d (%s): %zu tokens:", pass, pass < 2 ? "no repeats" : "repeats", toks.size());
       for (int t : toks) printf(" %d", t);
       printf("\n");
       outs.push_back(toks);
       mc_batch_destroy(bb);
     }
-    if (outs[0] != outs[1] || outs[2] != outs[3]) printf("note: persistent and multi-kernel steps differ\n");
+    if (outs[0] != outs[1] || outs[2] != outs[3]) { printf("repeated runs differ\n"); ++g_bad; }
     printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
     if (emu::oob_loads || emu::oob_stores) ++g_bad;
     printf("%s\n", g_bad ? "FAIL" : "OK");
@@ -126,7 +119,6 @@ int main(int argc, char** argv) {
     const int R = 12, W = 6;
     mc_batch* bb = nullptr;
     check(mc_batch_create(m, R, ctx, W - 1, &spec, &bb), "batch_create");
-    check(mc_batch_set_fused(bb, 0), "set_fused");
     or_model* om6 = or_model_create(&oc, SEED, ctx, R);
     uint64_t rng6 = 0x7777ull;
     auto toks6 = [&](int n) {
@@ -180,7 +172,6 @@ int main(int argc, char** argv) {
     or_forward(om, 1, &row0, &n, t.data(), nullptr);
     printf("prefill done\n");
   }
-  check(mc_batch_set_fused(b, cs == 1 || cs == 5 ? 0 : 2), "set_fused");
   const std::vector<int> widths = cs == 2 ? std::vector<int>{6} : std::vector<int>{6, 1, 8};
   for (int w : widths) {
     auto t = tokens(w);
