@@ -417,6 +417,7 @@ struct mc_batch {
   int32_t* moe_i32 = nullptr; // n_active per layer [L] | act_e [E] | off [E + 1] | pairs, sel [Mmax * TK]
   float* moe_wts = nullptr;   // [Mmax * TK]
   AttnWork aw{};
+  unsigned* attn_cnt = nullptr;  // [R * n_kv] split arrivals of the fused attention, zero at rest
   StepState s;
   void* scratch = nullptr;  // one allocation for the small StepState arrays
   // pinned staging
@@ -446,7 +447,7 @@ static void batch_free(mc_batch* b) {
   if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
-                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, b->scratch,
+                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, (void*)b->attn_cnt, b->scratch,
                   (void*)b->moe_xn, (void*)b->moe_logits, (void*)b->moe_act, (void*)b->moe_out, (void*)b->moe_i32,
                   (void*)b->moe_wts, (void*)b->xn})
     if (p) (void)hipFree(p);
@@ -558,7 +559,8 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
     }
     b->aw.nchunk = (max_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     if ((rc = dev_alloc(&b->aw.part_o, (size_t)M * nq * b->aw.nchunk * d)) ||
-        (rc = dev_alloc(&b->aw.part_ml, (size_t)M * nq * b->aw.nchunk * 2))) {
+        (rc = dev_alloc(&b->aw.part_ml, (size_t)M * nq * b->aw.nchunk * 2)) ||
+        (rc = dev_zero(&b->attn_cnt, (size_t)b->R * nkv))) {
       batch_free(b);
       return rc;
     }
@@ -790,17 +792,26 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   const int H = c.hidden, d = c.head_dim, nq = c.n_q_heads, nkv = c.n_kv_heads, I = c.intermediate;
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
+  // Attention with the q/k preparation and the split merge inside (one launch per layer
+  // instead of three) whenever a row's queries of one kv head fit its query buffer.
+  const bool fuse = attn_fuse_ok(b->R, nkv, b->aw.nchunk, max_q, nq, d);
   if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->ssq, H / 16, b->st)))
     return rc;
   for (int l = 0; l < c.n_layers; ++l) {
     const auto& L = m->layers[(size_t)l];
     if ((rc = run_gemv(b, L.qkv, b->x, H, L.in_norm, b->qkv, Nqkv, M, EPI_STORE))) return rc;
-    if ((rc = launch_qk_rope_append(b->qkv, L.q_norm, L.k_norm, b->rope_cos, b->rope_sin, M, nq, nkv, d, c.rms_eps,
-                                    s.slot_row, s.slot_pos, b->kv[(size_t)l], b->q, b->st)))
+    AttnFuse fz;
+    if (fuse) {
+      fz.qkv = b->qkv; fz.q_norm = L.q_norm; fz.k_norm = L.k_norm; fz.rope_cos = b->rope_cos; fz.rope_sin = b->rope_sin;
+      fz.eps = c.rms_eps; fz.counters = b->attn_cnt; fz.att = b->att;
+    } else if ((rc = launch_qk_rope_append(b->qkv, L.q_norm, L.k_norm, b->rope_cos, b->rope_sin, M, nq, nkv, d, c.rms_eps,
+                                           s.slot_row, s.slot_pos, b->kv[(size_t)l], b->q, b->st))) {
       return rc;
+    }
     size_t e0 = 0;
     if ((rc = prof_begin(b, &e0))) return rc;
-    if ((rc = launch_attention(b->q, b->kv[(size_t)l], sv, b->R, max_q, nq, nkv, d, M, b->aw, b->att, b->st)))
+    if ((rc = launch_attention(b->q, b->kv[(size_t)l], sv, b->R, max_q, nq, nkv, d, M, b->aw, fuse ? &fz : nullptr, b->att,
+                               b->st)))
       return rc;
     if ((rc = prof_end(b, e0, 1, 0.0))) return rc;
     if ((rc = run_gemv(b, L.o, b->att, nq * d, nullptr, b->x, H, M, EPI_RESIDUAL))) return rc;

@@ -201,6 +201,21 @@ __host__ __device__ inline uint32_t synth_scale_bias(uint64_t base, int n, int G
 }
 inline uint64_t synth_base(uint64_t seed, uint64_t tid) { return mix64(seed ^ mix64(tid)); }
 
+// Device-coherent 64-bit store / load (relaxed, agent scope: sc1 accesses).  Split-K and
+// split-KV partials travel through these: a store is written through to the device's
+// coherence point and a load misses the CU's L1, so a block on another XCD reads the
+// value once the writer's arrival (an agent-scope atomic issued after the store has
+// completed) is visible.
+__device__ inline void st_coherent(float* p, float a, float b) {
+  const unsigned long long v = (unsigned long long)__float_as_uint(a) | ((unsigned long long)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 ld_coherent(const float* p) {
+  const unsigned long long v =
+      __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
+}
+
 // Sum over the 8 lanes (l & ~7) .. + 7, the same value in each: DPP quad swaps (xor 1, xor 2),
 // then the half-row mirror (lane 7 - l of the other quad holds the other quad's sum).
 __device__ inline float sum8_lanes(float v) {

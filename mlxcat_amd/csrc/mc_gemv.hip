@@ -44,17 +44,6 @@ __device__ inline bf16x8 dequant_word(uint32_t w, uint32_t mask, uint32_t magic)
 
 __device__ inline float silu_f(float z) { return z / (1.0f + __expf(-z)); }
 
-// device-coherent 64-bit store / load (relaxed, agent scope: sc1 accesses)
-__device__ inline void st_coherent(float* p, float a, float b) {
-  const unsigned long long v = (unsigned long long)__float_as_uint(a) | ((unsigned long long)__float_as_uint(b) << 32);
-  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float2 ld_coherent(const float* p) {
-  const unsigned long long v =
-      __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
-}
-
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for
 // its outstanding global loads (__syncthreads would also drain the prefetched weights).
 __device__ inline void lds_barrier() {

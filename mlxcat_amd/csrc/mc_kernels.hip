@@ -78,9 +78,98 @@ __device__ inline float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// q/k RMSNorm (Qwen3) + rotate-half RoPE + KV append.  Grid (slot, head / 4), one
-// wave per head; lane i handles the rotation pair (i, i + d/2) for d = 128.
+// q/k RMSNorm (Qwen3) + rotate-half RoPE of one head vector by one wave: lane < d/2 holds
+// the rotation pair (lane, lane + d/2).  The standalone kernel below and the fused attention
+// both use it, so a key (or query) has the same bits whichever path computes it.  Products
+// are not contracted into fused multiply-adds: every step rounds where it is written.
 // ---------------------------------------------------------------------------
+__device__ inline void rope_pair(const uint16_t* hp, const uint16_t* nw, const float* rope_cos, const float* rope_sin,
+                                 int d, int pos, float eps, int lane, uint16_t* o1, uint16_t* o2) {
+#pragma clang fp contract(off)
+  const int hd = d >> 1;
+  float x1 = 0.f, x2 = 0.f;
+  if (lane < hd) {
+    x1 = bf16_to_f32(hp[lane]);
+    x2 = bf16_to_f32(hp[lane + hd]);
+  }
+  if (nw) {
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float r = 1.0f / sqrtf(ss / (float)d + eps);
+    if (lane < hd) {
+      x1 = bf16_to_f32(f32_to_bf16((x1 * r) * bf16_to_f32(nw[lane])));
+      x2 = bf16_to_f32(f32_to_bf16((x2 * r) * bf16_to_f32(nw[lane + hd])));
+    }
+  }
+  *o1 = *o2 = 0;
+  if (lane < hd) {
+    const float cs = rope_cos[(size_t)pos * hd + lane], sn = rope_sin[(size_t)pos * hd + lane];
+    *o1 = f32_to_bf16(x1 * cs - x2 * sn);
+    *o2 = f32_to_bf16(x1 * sn + x2 * cs);
+  }
+}
+
+// QB head vectors per wave at once (independent latency chains), each with rope_pair's
+// arithmetic, in two steps so that a caller can issue other loads in between: rope_load
+// issues the loads of vector i (hp[i] at position pos[i]; ok[i] false leaves it out) and
+// rope_finish normalises and rotates them.
+template <int QB>
+struct RopeRegs {
+  float x1[QB], x2[QB], cs[QB], sn[QB], w1, w2;
+};
+
+template <int QB>
+__device__ inline void rope_load(RopeRegs<QB>& g, const uint16_t* const (&hp)[QB], const int (&pos)[QB],
+                                 const bool (&ok)[QB], const uint16_t* nw, const float* rope_cos,
+                                 const float* rope_sin, int d, int lane) {
+  const int hd = d >> 1;
+  g.w1 = g.w2 = 0.f;
+  if (nw && lane < hd) {
+    g.w1 = bf16_to_f32(nw[lane]);
+    g.w2 = bf16_to_f32(nw[lane + hd]);
+  }
+#pragma unroll
+  for (int i = 0; i < QB; ++i) {
+    g.x1[i] = g.x2[i] = g.cs[i] = g.sn[i] = 0.f;
+    if (ok[i] && lane < hd) {
+      g.x1[i] = bf16_to_f32(hp[i][lane]);
+      g.x2[i] = bf16_to_f32(hp[i][lane + hd]);
+      g.cs[i] = rope_cos[(size_t)pos[i] * hd + lane];
+      g.sn[i] = rope_sin[(size_t)pos[i] * hd + lane];
+    }
+  }
+}
+
+template <int QB>
+__device__ inline void rope_finish(RopeRegs<QB>& g, bool norm, int d, float eps, int lane, uint16_t (&o1)[QB],
+                                   uint16_t (&o2)[QB]) {
+#pragma clang fp contract(off)
+  const int hd = d >> 1;
+  if (norm) {
+    float ss[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) ss[i] = g.x1[i] * g.x1[i] + g.x2[i] * g.x2[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+      for (int i = 0; i < QB; ++i) ss[i] += __shfl_xor(ss[i], o);
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+      const float r = 1.0f / sqrtf(ss[i] / (float)d + eps);
+      if (lane < hd) {
+        g.x1[i] = bf16_to_f32(f32_to_bf16((g.x1[i] * r) * g.w1));
+        g.x2[i] = bf16_to_f32(f32_to_bf16((g.x2[i] * r) * g.w2));
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < QB; ++i) {
+    o1[i] = f32_to_bf16(g.x1[i] * g.cs[i] - g.x2[i] * g.sn[i]);
+    o2[i] = f32_to_bf16(g.x1[i] * g.sn[i] + g.x2[i] * g.cs[i]);
+  }
+}
+
+// Grid (slot, head / 4), one wave per head: q heads to q_out, k heads and v heads appended
+// to the cache at the slot's position.
 __global__ void __launch_bounds__(256) qk_rope_append_kernel(const uint16_t* qkv, const uint16_t* q_norm,
                                                              const uint16_t* k_norm, const float* rope_cos,
                                                              const float* rope_sin, int nq, int nkv, int d,
@@ -92,49 +181,24 @@ __global__ void __launch_bounds__(256) qk_rope_append_kernel(const uint16_t* qkv
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hd = d >> 1;
   const int ntot = nq + 2 * nkv;
-  const int Nqkv = ntot * d;
-  const uint16_t* src = qkv + (size_t)m * Nqkv;
-  {
-    const int hh = blockIdx.y * 4 + wave;  // one wave per head
-    if (hh >= ntot) return;
-    const uint16_t* hp = src + (size_t)hh * d;
-    if (hh >= nq + nkv) {  // V head: copy into the cache
-      const int h = hh - nq - nkv;
-      uint16_t* dst = kv.v + ((size_t)row * nkv + h) * d * kv.cap + pos;
-      for (int i = lane; i < d; i += 64) dst[(size_t)i * kv.cap] = hp[i];
-      return;
-    }
-    const bool is_q = hh < nq;
-    const uint16_t* nw = is_q ? q_norm : k_norm;
-    // d <= 128: lane < hd handles (lane, lane + hd)
-    float x1 = 0.f, x2 = 0.f;
-    if (lane < hd) {
-      x1 = bf16_to_f32(hp[lane]);
-      x2 = bf16_to_f32(hp[lane + hd]);
-    }
-    if (nw) {
-      const float ss = wave_sum(x1 * x1 + x2 * x2);
-      const float r = 1.0f / sqrtf(ss / (float)d + eps);
-      if (lane < hd) {
-        x1 = bf16_to_f32(f32_to_bf16((x1 * r) * bf16_to_f32(nw[lane])));
-        x2 = bf16_to_f32(f32_to_bf16((x2 * r) * bf16_to_f32(nw[lane + hd])));
-      }
-    }
-    if (lane < hd) {
-      const float cs = rope_cos[(size_t)pos * hd + lane], sn = rope_sin[(size_t)pos * hd + lane];
-      const uint16_t o1 = f32_to_bf16(x1 * cs - x2 * sn);
-      const uint16_t o2 = f32_to_bf16(x1 * sn + x2 * cs);
-      if (is_q) {
-        uint16_t* dst = q_out + (size_t)m * nq * d + (size_t)hh * d;
-        dst[lane] = o1;
-        dst[lane + hd] = o2;
-      } else {
-        const int h = hh - nq;
-        uint16_t* dst = kv.k + (((size_t)row * nkv + h) * kv.cap + pos) * d;
-        dst[lane] = o1;
-        dst[lane + hd] = o2;
-      }
-    }
+  const uint16_t* src = qkv + (size_t)m * ntot * d;
+  const int hh = blockIdx.y * 4 + wave;  // one wave per head
+  if (hh >= ntot) return;
+  const uint16_t* hp = src + (size_t)hh * d;
+  if (hh >= nq + nkv) {  // V head: copy into the cache
+    const int h = hh - nq - nkv;
+    uint16_t* dst = kv.v + ((size_t)row * nkv + h) * d * kv.cap + pos;
+    for (int i = lane; i < d; i += 64) dst[(size_t)i * kv.cap] = hp[i];
+    return;
+  }
+  const bool is_q = hh < nq;
+  uint16_t o1, o2;
+  rope_pair(hp, is_q ? q_norm : k_norm, rope_cos, rope_sin, d, pos, eps, lane, &o1, &o2);
+  if (lane < hd) {
+    uint16_t* dst = is_q ? q_out + (size_t)m * nq * d + (size_t)hh * d
+                         : kv.k + (((size_t)row * nkv + (hh - nq)) * kv.cap + pos) * d;
+    dst[lane] = o1;
+    dst[lane + hd] = o2;
   }
 }
 
@@ -168,10 +232,62 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 constexpr int FA_TP = 2;  // query tiles of 16 per pass
 
-template <int D>
+// Merge of one query's split partials 0 .. ns - 1, in split order, for the output element
+// pair (e0, e0 + 1): running max, rescaled sums (the arithmetic of the standalone merge
+// kernel below, shared by the last-arriving block of the fused attention).
+template <bool COHERENT>
+__device__ inline float2 merge_splits(const float* pml, const float* po, int ns, int d, int e0) {
+  float mx = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
+  constexpr int UN = 8;
+  for (int c0 = 0; c0 < ns; c0 += UN) {
+    float2 ml[UN], ov[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int cc = c0 + u;
+      ml[u] = make_float2(-INFINITY, 0.f);
+      ov[u] = make_float2(0.f, 0.f);
+      if (cc < ns) {
+        ml[u] = COHERENT ? ld_coherent(pml + (size_t)cc * 2) : *reinterpret_cast<const float2*>(pml + (size_t)cc * 2);
+        if (e0 < d)
+          ov[u] = COHERENT ? ld_coherent(po + (size_t)cc * d + e0) : *reinterpret_cast<const float2*>(po + (size_t)cc * d + e0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const float cm = ml[u].x;
+      if (cm == -INFINITY) continue;  // a split with no visible key
+      const float nm = fmaxf(mx, cm);
+      const float fo = (mx == -INFINITY) ? 0.f : __expf(mx - nm);
+      const float fn = __expf(cm - nm);
+      l = l * fo + ml[u].y * fn;
+      a0 = a0 * fo + ov[u].x * fn;
+      a1 = a1 * fo + ov[u].y * fn;
+      mx = nm;
+    }
+  }
+  const float inv = 1.0f / l;
+  return make_float2(a0 * inv, a1 * inv);
+}
+
+// FUSE: the block also prepares its queries and the new keys, and the splits are merged by
+// the last block of each (row, kv head) to arrive:
+//   * q rows of the row's queries of this kv head (q-norm + RoPE, rope_pair) into LDS;
+//   * the new keys / values whose positions fall in this block's key range (k-norm + RoPE)
+//     appended to the cache, read back by the block's own waves after a barrier (each new
+//     position lies in exactly one block's range);
+//   * the block's partials stored device-coherent; an agent-scope arrival count per
+//     (row, kv head); the last arrival merges every split in split order into att (the
+//     standalone merge's arithmetic) and rearms the count.
+// Queries and keys have the same bits as the standalone preparation kernel's; the merge
+// weights each split by exp(m_sp - M) / L in one pass (the standalone merge rescales a running
+// sum split by split), so attention outputs agree with the three-kernel path to rounding.
+
+template <int D, bool FUSE>
 __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLayer kv, SlotView sv, int nq, int nkv,
-                                                         float scale, int S, AttnWork w) {
+                                                         float scale, int S, AttnWork w, AttnFuse f) {
   __shared__ float mrg[4][FA_TP][16][D + 2];  // per wave: o[d], max, sum of each query of the pass
+  __shared__ __align__(16) uint16_t qs[FUSE ? FUSE_QMAX * D : 8];
+  __shared__ int s_last;
   const int G = nq / nkv;
   const int r = blockIdx.x / nkv, kh = blockIdx.x % nkv;
   const int split = blockIdx.y;
@@ -190,6 +306,110 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
   const uint16_t* vbase = kv.v + head * D * kv.cap;   // [d][pos]
   constexpr int NS = D / 32, NDB = D / 16;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  // keys sc .. sc + 63 of the cache (inside the row's cap; keys >= kend are finite and masked)
+  bf16x8_t ka[4][4];
+  s16x4_t va[NDB][4];
+  auto load_kv = [&](int sc) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        ka[kb][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)(sc + 16 * kb + r16) * D + 32 * s4 + 8 * c)
+                             : __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        va[db][kb] = *reinterpret_cast<const s16x4_t*>(vbase + (size_t)(16 * db + r16) * kv.cap + sc + 16 * kb + 4 * c);
+  };
+  const int sc_first = s0 + ATTN_CHUNK * wave;
+  bool pre = false;  // this wave's first sub-chunk is already in registers
+  if constexpr (FUSE) {
+    // loads of the prologue first (the queries of this wave, the new keys / values), then the
+    // first sub-chunk of cached keys when it holds no key of this step: the normalisation and
+    // rotation below wait only for the former (loads retire in order)
+    const size_t ldq = (size_t)(nq + 2 * nkv) * D;  // row stride of the qkv projections
+    constexpr int HD = D / 2, QB = FUSE_QMAX / 4, KB = 4;
+    const uint16_t* hq[QB];
+    int pq[QB];
+    bool oq[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {  // queries wave + 4 i
+      const int qi = wave + 4 * i;
+      oq[i] = qi < nqry;
+      const int qc = oq[i] ? qi : 0;
+      const int j = qc / G, gh = qc - j * G;
+      hq[i] = f.qkv + (size_t)(slot0 + j) * ldq + (size_t)(kh * G + gh) * D;
+      pq[i] = base + j;
+    }
+    RopeRegs<QB> gq;
+    rope_load<QB>(gq, hq, pq, oq, f.q_norm, f.rope_cos, f.rope_sin, D, lane);
+    // the new keys and values in this block's key range: positions p0 + wave + 4 i
+    const int p0 = max(s0, base);
+    const uint16_t* hk[KB];
+    int pk[KB];
+    bool ok[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int p = p0 + wave + 4 * i;
+      ok[i] = p < s1;
+      pk[i] = ok[i] ? p : p0;
+      hk[i] = f.qkv + (size_t)(slot0 + pk[i] - base) * ldq + (size_t)(nq + kh) * D;
+    }
+    RopeRegs<KB> gk;
+    uint16_t vv[KB][D / 64];
+    if (p0 < s1) {
+      rope_load<KB>(gk, hk, pk, ok, f.k_norm, f.rope_cos, f.rope_sin, D, lane);
+#pragma unroll
+      for (int i = 0; i < KB; ++i)
+#pragma unroll
+        for (int e = 0; e < D / 64; ++e) vv[i][e] = ok[i] ? hk[i][(size_t)nkv * D + lane + 64 * e] : (uint16_t)0;
+    }
+    pre = sc_first < s1 && sc_first + ATTN_CHUNK <= base;
+    if (pre) load_kv(sc_first);
+    uint16_t o1[QB], o2[QB];
+    rope_finish<QB>(gq, f.q_norm != nullptr, D, f.eps, lane, o1, o2);
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+      const int qi = wave + 4 * i;
+      if (oq[i] && lane < HD) {
+        qs[qi * D + lane] = o1[i];
+        qs[qi * D + lane + HD] = o2[i];
+      }
+    }
+    // batch b of new positions: p0 + 4 KB b + wave + 4 i (the first batch's loads are above)
+    uint16_t* kw = kv.k + head * kv.cap * D;
+    uint16_t* vw = kv.v + head * D * kv.cap;
+    for (int b0 = p0; b0 < s1; b0 += 4 * KB) {
+      if (b0 != p0) {
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+          const int p = b0 + wave + 4 * i;
+          ok[i] = p < s1;
+          pk[i] = ok[i] ? p : p0;
+          hk[i] = f.qkv + (size_t)(slot0 + pk[i] - base) * ldq + (size_t)(nq + kh) * D;
+        }
+        rope_load<KB>(gk, hk, pk, ok, f.k_norm, f.rope_cos, f.rope_sin, D, lane);
+#pragma unroll
+        for (int i = 0; i < KB; ++i)
+#pragma unroll
+          for (int e = 0; e < D / 64; ++e) vv[i][e] = ok[i] ? hk[i][(size_t)nkv * D + lane + 64 * e] : (uint16_t)0;
+      }
+      uint16_t k1[KB], k2[KB];
+      rope_finish<KB>(gk, f.k_norm != nullptr, D, f.eps, lane, k1, k2);
+#pragma unroll
+      for (int i = 0; i < KB; ++i) {
+        if (!ok[i]) continue;
+        if (lane < HD) {
+          kw[(size_t)pk[i] * D + lane] = k1[i];
+          kw[(size_t)pk[i] * D + lane + HD] = k2[i];
+        }
+#pragma unroll
+        for (int e = 0; e < D / 64; ++e) vw[(size_t)(lane + 64 * e) * kv.cap + pk[i]] = vv[i][e];
+      }
+    }
+    __syncthreads();  // the queries and this range's new keys are visible to every wave
+  }
   const int nqt = (nqry + 15) / 16;
   for (int t0 = 0; t0 < nqt; t0 += FA_TP) {
     // B operands: q rows of queries (t0 + tt) 16 + r16, d = 32 s + 8 c .. + 7
@@ -200,7 +420,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
       const int qi = min((t0 + tt) * 16 + r16, nqry - 1);
       const int j = qi / G, gh = qi - j * G;
       qpos[tt] = (t0 + tt) * 16 + r16 < nqry ? base + j : -1;
-      const uint16_t* qp = q + ((size_t)(slot0 + j) * nq + kh * G + gh) * D;
+      const uint16_t* qp = FUSE ? qs + (size_t)qi * D : q + ((size_t)(slot0 + j) * nq + kh * G + gh) * D;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
         qb[tt][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * s4 + 8 * c)
@@ -215,21 +435,8 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
 #pragma unroll
       for (int db = 0; db < NDB; ++db) o[tt][db] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
     }
-    for (int sc = s0 + ATTN_CHUNK * wave; sc < s1; sc += 4 * ATTN_CHUNK) {
-      // keys sc .. sc + 63 (inside the row's cap; keys >= kend are finite and masked)
-      bf16x8_t ka[4][4];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-          ka[kb][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)(sc + 16 * kb + r16) * D + 32 * s4 + 8 * c)
-                               : __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
-      s16x4_t va[NDB][4];
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-          va[db][kb] = *reinterpret_cast<const s16x4_t*>(vbase + (size_t)(16 * db + r16) * kv.cap + sc + 16 * kb + 4 * c);
+    for (int sc = sc_first; sc < s1; sc += 4 * ATTN_CHUNK) {
+      if (!(pre && t0 == 0 && sc == sc_first)) load_kv(sc);
 #pragma unroll
       for (int tt = 0; tt < FA_TP; ++tt) {
         if (t0 + tt >= nqt) break;
@@ -313,28 +520,114 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
         float mx = -INFINITY;
 #pragma unroll
         for (int w2 = 0; w2 < 4; ++w2) mx = fmaxf(mx, mrg[w2][tt][qq][D]);
-        float f[4], l = 0.f;
+        float fw[4], l = 0.f;
 #pragma unroll
         for (int w2 = 0; w2 < 4; ++w2) {
           const float m2 = mrg[w2][tt][qq][D];
-          f[w2] = m2 == -INFINITY ? 0.f : __expf(m2 - mx);
-          l += mrg[w2][tt][qq][D + 1] * f[w2];
+          fw[w2] = m2 == -INFINITY ? 0.f : __expf(m2 - mx);
+          l += mrg[w2][tt][qq][D + 1] * fw[w2];
         }
         const int jj = qi / G, gg = qi - jj * G;
         const size_t pidx = ((size_t)(slot0 + jj) * nq + kh * G + gg) * w.nchunk + split;
-        for (int e = part * (D / 8); e < (part + 1) * (D / 8); ++e) {
-          float a = 0.f;
+        for (int e = part * (D / 8); e < (part + 1) * (D / 8); e += 2) {
+          float a[2] = {0.f, 0.f};
 #pragma unroll
-          for (int w2 = 0; w2 < 4; ++w2) a += mrg[w2][tt][qq][e] * f[w2];
-          w.part_o[pidx * D + e] = a;
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int w2 = 0; w2 < 4; ++w2) a[h] += mrg[w2][tt][qq][e + h] * fw[w2];
+          if constexpr (FUSE) st_coherent(w.part_o + pidx * D + e, a[0], a[1]);
+          else {
+            w.part_o[pidx * D + e] = a[0];
+            w.part_o[pidx * D + e + 1] = a[1];
+          }
         }
         if (part == 0) {
-          w.part_ml[pidx * 2] = mx;
-          w.part_ml[pidx * 2 + 1] = l;
+          if constexpr (FUSE) st_coherent(w.part_ml + pidx * 2, mx, l);
+          else {
+            w.part_ml[pidx * 2] = mx;
+            w.part_ml[pidx * 2 + 1] = l;
+          }
         }
       }
     }
     __syncthreads();
+  }
+  if constexpr (FUSE) {
+    // arrival of this split (its partial stores complete first); the last one merges
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int nsplit = (kend + S * ATTN_CHUNK - 1) / (S * ATTN_CHUNK);
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(f.counters + head, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (threadIdx.x == 0) __hip_atomic_store(f.counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Split sp of query qi gets the weight exp(m_sp - M) (M: the query's largest split max)
+    // and the query 1 / L, L = sum_sp l_sp exp(m_sp - M); a query at position p holds keys in
+    // splits 0 .. p / (S 64) only.  (m, l) of every (query, split) go to LDS first (one load
+    // each, all in flight), the weights replace them, then every output element sums its
+    // splits' partials with all of a batch's loads in flight.  The pass buffer is free.
+    float2* mls = reinterpret_cast<float2*>(&mrg[0][0][0][0]);  // [nqry][nsplit]
+    float* invl = reinterpret_cast<float*>(mls + nqry * nsplit);
+    for (int i = threadIdx.x; i < nqry * nsplit; i += 256) {
+      const int qi = i / nsplit, sp = i - qi * nsplit;
+      const int jj = qi / G, gg = qi - jj * G;
+      const size_t qh = (size_t)(slot0 + jj) * nq + kh * G + gg;
+      mls[i] = sp <= (base + jj) / (S * ATTN_CHUNK) ? ld_coherent(w.part_ml + (qh * w.nchunk + sp) * 2)
+                                                   : make_float2(-INFINITY, 0.f);
+    }
+    __syncthreads();
+    for (int qi = threadIdx.x; qi < nqry; qi += 256) {
+      float2* q2 = mls + qi * nsplit;
+      float mx = -INFINITY;
+      for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, q2[sp].x);
+      float l = 0.f;
+      for (int sp = 0; sp < nsplit; ++sp) {
+        const float e = q2[sp].x == -INFINITY ? 0.f : __expf(q2[sp].x - mx);
+        l += q2[sp].y * e;
+        q2[sp].x = e;
+      }
+      invl[qi] = 1.0f / l;
+    }
+    __syncthreads();
+    // thread per (query, 4 elements): the splits' float4 partials, NB per round in flight
+    constexpr int NB = 24;
+    for (int it = threadIdx.x; it < nqry * (D / 4); it += 256) {
+      const int qi = it / (D / 4), e0 = (it - qi * (D / 4)) * 4;
+      const int jj = qi / G, gg = qi - jj * G;
+      const size_t qh = (size_t)(slot0 + jj) * nq + kh * G + gg;
+      const float* po = w.part_o + qh * w.nchunk * D + e0;
+      const float2* q2 = mls + qi * nsplit;
+      const int ns = (base + jj) / (S * ATTN_CHUNK) + 1;
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int c0 = 0; c0 < ns; c0 += NB) {
+        float2 ov[NB][2];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          ov[u][0] = ov[u][1] = make_float2(0.f, 0.f);
+          if (c0 + u < ns) {
+            ov[u][0] = ld_coherent(po + (size_t)(c0 + u) * D);
+            ov[u][1] = ld_coherent(po + (size_t)(c0 + u) * D + 2);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          if (c0 + u >= ns) break;
+          const float e = q2[c0 + u].x;
+          acc[0] += ov[u][0].x * e;
+          acc[1] += ov[u][0].y * e;
+          acc[2] += ov[u][1].x * e;
+          acc[3] += ov[u][1].y * e;
+        }
+      }
+      const float il = invl[qi];
+      uint2 o;
+      o.x = (uint32_t)f32_to_bf16(acc[0] * il) | ((uint32_t)f32_to_bf16(acc[1] * il) << 16);
+      o.y = (uint32_t)f32_to_bf16(acc[2] * il) | ((uint32_t)f32_to_bf16(acc[3] * il) << 16);
+      *reinterpret_cast<uint2*>(f.att + qh * D + e0) = o;
+    }
   }
 }
 
@@ -353,57 +646,49 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(SlotView sv, int M, int
     return;
   }
   const int ns = sv.slot_pos[m] / (S * ATTN_CHUNK) + 1;
-  const float* pml = w.part_ml + ((size_t)m * nq + h) * w.nchunk * 2;
-  const float* po = w.part_o + ((size_t)m * nq + h) * w.nchunk * d;
-  float mx = -INFINITY, l = 0.f, a0 = 0.f, a1 = 0.f;
-  constexpr int UN = 8;
-  for (int c0 = 0; c0 < ns; c0 += UN) {
-    float2 ml[UN], ov[UN];
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int cc = c0 + u;
-      ml[u] = make_float2(-INFINITY, 0.f);
-      ov[u] = make_float2(0.f, 0.f);
-      if (cc < ns) {
-        ml[u] = *reinterpret_cast<const float2*>(pml + (size_t)cc * 2);
-        if (e0 < d) ov[u] = *reinterpret_cast<const float2*>(po + (size_t)cc * d + e0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const float cm = ml[u].x;
-      if (cm == -INFINITY) continue;  // a split with no visible key
-      const float nm = fmaxf(mx, cm);
-      const float fo = (mx == -INFINITY) ? 0.f : __expf(mx - nm);
-      const float fn = __expf(cm - nm);
-      l = l * fo + ml[u].y * fn;
-      a0 = a0 * fo + ov[u].x * fn;
-      a1 = a1 * fo + ov[u].y * fn;
-      mx = nm;
-    }
-  }
-  if (e0 < d) {
-    const float inv = 1.0f / l;
-    *reinterpret_cast<uint32_t*>(out + e0) = (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
-  }
+  const size_t qh = (size_t)m * nq + h;
+  const float2 o = merge_splits<false>(w.part_ml + qh * w.nchunk * 2, w.part_o + qh * w.nchunk * d, ns, d, e0);
+  if (e0 < d) *reinterpret_cast<uint32_t*>(out + e0) = (uint32_t)f32_to_bf16(o.x) | ((uint32_t)f32_to_bf16(o.y) << 16);
+}
+
+// 64-key sub-chunks per block: more when the grid would exceed about 1024 blocks (fewer
+// partials to merge), at least 8 from 64 (row, kv head) pairs on (two sub-chunks per wave,
+// 4x fewer partials; batch 8 at 2K keys 5.08 -> 4.89 ms per step, 8 rows at 512-4096 keys
+// 6.71 -> 6.28 ms), else 2: a decode row spreads its heads over more CUs (a block's loads
+// are one latency-bound round; at 2K keys the fused kernel's loads took 3.7 us with 2
+// sub-chunks per block and 6.1 us with 4).
+int attn_split(int R, int nkv, int nchunk, bool fused) {
+  const int smin = R * nkv >= 64 ? 8 : 2;
+  return std::max(smin, (R * nkv * nchunk + 1023) / 1024);
+}
+
+bool attn_fuse_ok(int R, int nkv, int nchunk, int max_q, int nq, int d) {
+  if (max_q * (nq / nkv) > FUSE_QMAX) return false;
+  // the merging block keeps (m, l) per (query, split) and 1 / L per query in the pass buffer
+  const int S = attn_split(R, nkv, nchunk, true);
+  const size_t words = (size_t)FUSE_QMAX * (2 * ((nchunk + S - 1) / S) + 1);
+  return words <= (size_t)4 * FA_TP * 16 * (d + 2);
 }
 
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
-                     int M, const AttnWork& w, uint16_t* att, hipStream_t st) {
+                     int M, const AttnWork& w, const AttnFuse* fuse, uint16_t* att, hipStream_t st) {
   if (d != 64 && d != 128) return fail(MC_E_INVALID, "attention: head_dim must be 64 or 128");
-  (void)max_q;
+  if (fuse && (!attn_fuse_ok(R, nkv, w.nchunk, max_q, nq, d) || !fuse->qkv || !fuse->counters || !fuse->att))
+    return fail(MC_E_INVALID, "attention: the fused path takes at most 64 queries per (row, kv head)");
   const float scale = 1.0f / sqrtf((float)d);
-  // 64-key sub-chunks per block: more when the grid would exceed about 1024 blocks (fewer
-  // partials to merge), and at least 2 (a few (row, kv head) pairs: one decode row spreads
-  // its 8 heads over more CUs, 10.0 -> 8.0 us per layer at 2K keys against 4) or 8 (64 or
-  // more pairs: two sub-chunks per wave, 4x fewer partials; batch 8 at 2K keys
-  // 5.08 -> 4.89 ms per step, 8 rows at 512-4096 keys 6.71 -> 6.28 ms).
-  const int smin = R * nkv >= 64 ? 8 : 2;
-  const int S = std::max(smin, (R * nkv * w.nchunk + 1023) / 1024);
+  const int S = attn_split(R, nkv, w.nchunk, fuse != nullptr);
   const dim3 grid(R * nkv, (w.nchunk + S - 1) / S);
-  if (d == 128) hipLaunchKernelGGL(attn_flash_kernel<128>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
-  else hipLaunchKernelGGL(attn_flash_kernel<64>, grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w);
+  const AttnFuse nf{};
+  const AttnFuse& f = fuse ? *fuse : nf;
+  if (d == 128) {
+    if (fuse) hipLaunchKernelGGL((attn_flash_kernel<128, true>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    else hipLaunchKernelGGL((attn_flash_kernel<128, false>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+  } else {
+    if (fuse) hipLaunchKernelGGL((attn_flash_kernel<64, true>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    else hipLaunchKernelGGL((attn_flash_kernel<64, false>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+  }
   MC_HIP(hipGetLastError());
+  if (fuse) return MC_OK;
   hipLaunchKernelGGL(attn_merge_kernel, dim3((M * nq + 3) / 4), dim3(256), 0, st, sv, M, nq, d, S, w, att);
   MC_HIP(hipGetLastError());
   return MC_OK;

@@ -39,8 +39,25 @@ struct AttnWork {
   int nchunk;      // ceil(cap / ATTN_CHUNK)
 };
 constexpr int ATTN_CHUNK = 64;
+// The fused path (fuse != NULL): the attention blocks also do the q/k-norm + RoPE of their
+// queries and append the new keys (no launch_qk_rope_append), and the last block of each
+// (row, kv head) merges the splits (no merge launch).  At most 64 queries per (row, kv head).
+constexpr int FUSE_QMAX = 64;
+struct AttnFuse {
+  const uint16_t* qkv = nullptr;     // [M][(nq + 2 nkv) d] projections of the slots
+  const uint16_t* q_norm = nullptr;  // [d] (NULL: no q/k norm, Llama)
+  const uint16_t* k_norm = nullptr;
+  const float* rope_cos = nullptr;   // [pos][d / 2]
+  const float* rope_sin = nullptr;
+  float eps = 0.f;
+  unsigned* counters = nullptr;      // [R * nkv] split arrivals, zero at rest
+  uint16_t* att = nullptr;           // [M][nq d]
+};
+// 64-key sub-chunks per attention block; whether the fused path serves a call
+int attn_split(int R, int nkv, int nchunk, bool fused);
+bool attn_fuse_ok(int R, int nkv, int nchunk, int max_q, int nq, int d);
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
-                     int M, const AttnWork& w, uint16_t* att, hipStream_t st);
+                     int M, const AttnWork& w, const AttnFuse* fuse, uint16_t* att, hipStream_t st);
 
 int launch_fake_logits(int arch, const int32_t* slot_tok, int M, int V, uint16_t* logits, hipStream_t st);
 

@@ -174,3 +174,18 @@ def test_verify_logits_are_m_invariant(hip):
     np.testing.assert_array_equal(la, lb)
     for layer in range(2):
         np.testing.assert_array_equal(a.read_kv(layer, 0, 0), b.read_kv(layer, 0, 0))
+
+
+def test_fused_attention_many_new_keys(hip, oracle):
+    """A 30-token call of the tiny model (GQA 2: 60 queries per kv head) takes the fused
+    attention path, whose blocks append more new keys than one batch of their waves (16)
+    covers; its logits and every appended key and value against the oracle."""
+    gm, gb, om = pair(hip, oracle, TINY, rows=1, ctx=256)
+    rng = np.random.default_rng(7)
+    for n in (30, 6, 29):
+        toks = rng.integers(0, 4096, n).tolist()
+        assert_close_bf16(gb.forward([0], [n], toks), om.forward([0], [n], toks), what=f"call of {n}")
+    assert gb.kv_len(0) == om.kv_len(0) == 65
+    for layer in range(TINY["n_layers"]):
+        for w in (0, 1):
+            assert_close_bf16_kv(gb.read_kv(layer, 0, w), om.kv(layer, 0, w), what=f"kv {layer} {w}")
