@@ -187,3 +187,54 @@ def test_capacity_errors_are_loud(hip):
         b.insert(0, list(range(1, 30)), 10, hip.make_sampling())
     with pytest.raises(hip.HipError):
         b.forward([0], [40], list(range(40)))
+
+
+def _oracle_run(oracle, cfg, spec_cfg, prompts, max_tokens, samplings):
+    om = oracle.Model(cfg, SEED, 256, len(prompts))
+    og = oracle.Generator(om, spec_cfg, len(prompts), 256)
+    out = {}
+    for r, p in enumerate(prompts):
+        tok, _ = og.insert(r, p, max_tokens[r], samplings[r])
+        out[r] = [tok]
+    while any(og.active(r) for r in range(len(prompts))):
+        t, c, f = og.step()
+        for r in range(len(prompts)):
+            out[r] += t[r, :c[r]].tolist()
+    return out, og.stats()
+
+
+def test_single_row_gate_matches_oracle(hip, oracle):
+    """The reference speculates only while exactly one row runs (rowUIDs.count == 1,
+    BatchGenerator.swift:959): two active rows make no proposals; once the short row
+    finishes, the remaining row speculates.  Tokens and stats equal the oracle's."""
+    sp_cfg = spec(k=4, min_ctx=8, acceptance=0, single_row_only=1, greedy_only=1)
+    mt = [4, 12]
+    got, st, _, _, _ = gen_gpu(hip, FAKE_REPEATING, sp_cfg, [PROMPT, PROMPT], mt)
+    want, ost = _oracle_run(oracle, FAKE_REPEATING, sp_cfg, [PROMPT, PROMPT], mt,
+                            [oracle.make_sampling(), oracle.make_sampling()])
+    assert got == want
+    assert st == ost
+    assert 0 < st["proposal_batches"]
+    # while both rows ran (the first 3 steps) nothing was proposed: every token of the short
+    # row came from plain decodes, one per step
+    assert len(got[0]) == 4
+    both = dict(st)
+    alone, st2, _, _, _ = gen_gpu(hip, FAKE_REPEATING, sp_cfg, [PROMPT], [12])
+    assert alone[0] == got[1]
+    assert both["proposed"] < st2["proposed"]
+
+
+def test_greedy_gate_matches_oracle(hip, oracle):
+    """Rows with temperature > 0 or a seed do not speculate under the reference gate
+    (BatchGenerator.swift:963,970); greedy rows beside them do.  Against the oracle."""
+    sp_cfg = spec(k=4, min_ctx=8, acceptance=1, single_row_only=0, greedy_only=1)
+    mt = [12, 12, 12]
+    sps = [hip.make_sampling(), hip.make_sampling(temperature=0.8, seed=3), hip.make_sampling(seed=4)]
+    osps = [oracle.make_sampling(), oracle.make_sampling(temperature=0.8, seed=3), oracle.make_sampling(seed=4)]
+    got, st, _, _, _ = gen_gpu(hip, FAKE_REPEATING, sp_cfg, [PROMPT] * 3, mt, samplings=sps)
+    want, ost = _oracle_run(oracle, FAKE_REPEATING, sp_cfg, [PROMPT] * 3, mt, osps)
+    assert got == want
+    assert st == ost
+    # only the greedy, unseeded row proposes: its two batches, as when it runs alone
+    alone, st1, _, _, _ = gen_gpu(hip, FAKE_REPEATING, sp_cfg, [PROMPT], [12])
+    assert st["proposal_batches"] == st1["proposal_batches"] > 0
