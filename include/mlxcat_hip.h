@@ -98,7 +98,12 @@ typedef struct mc_spec_config {
   int32_t greedy_only;         /* reference gate temperature == 0 && no RNG (:963,970) */
 } mc_spec_config;
 
-/* Subset of SamplingParameters (Sources/MLXCat/TrackB/Sampling.swift:139-217) used by the step. */
+/* Subset of SamplingParameters (Sources/MLXCat/TrackB/Sampling.swift:139-217) used by the step.
+ * Per position the sampler sees the bf16 logits in fp32 after the logit bias and the
+ * min_tokens EOS mask (Sampling.swift:638-652) and the penalties over the generated tokens
+ * (:592-636); greedy rows take the argmax of those values, sampled rows filter them with
+ * top-p, min-p and top-k in that order (:500-522) and scale by 1 / temperature.  A
+ * zero-filled struct is plain greedy decoding. */
 typedef struct mc_sampling {
   float temperature;   /* 0 = greedy argmax, lowest index on ties */
   float top_p;         /* applied when 0 < top_p < 1, Sampling.swift:847-858 */
@@ -107,6 +112,15 @@ typedef struct mc_sampling {
   int32_t n_eos;
   int32_t eos[8];
   int32_t reject_token; /* tool-call trigger (BatchGenerator.swift:920-923); -1 = none */
+  int32_t top_k;        /* 0 = off; ties at the k-th value keep the lowest token ids */
+  float min_p;          /* 0 = off; keeps values v with v - max >= log(min_p) */
+  float repetition_penalty; /* 1 = off; 0 is read as 1 */
+  float presence_penalty;   /* 0 = off */
+  float frequency_penalty;  /* 0 = off */
+  int32_t min_tokens;   /* EOS ids masked while fewer tokens were generated */
+  int32_t n_bias;       /* logit bias entries (at most 16; ids outside the vocabulary ignored) */
+  int32_t bias_token[16];
+  float bias_value[16];
 } mc_sampling;
 
 /* SpeculativeDecodingStats, BatchGenerator.swift:31-38 */
@@ -185,14 +199,18 @@ int mc_ngram_propose(const int32_t* hist, const int64_t* hist_off, int32_t B,
 
 /* ---- acceptance: the loop over TokenSampler.sample at BatchGenerator.swift:906-935,
  * run on the GPU over host logits.  Per row r: logits rows [row_off[r], row_off[r] +
- * n_draft[r] + 1), drafts[r][0..n_draft[r]).  Greedy rows use `acceptance`; rows with
- * temperature > 0 use speculative sampling with 32-bit uniforms derived from
- * (seed, counter[r]).  Outputs: n_emit[r] tokens in out_tokens[r][0 .. draft_stride],
- * (row stride draft_stride + 1), kv_keep[r] positions of the verified block to keep,
- * n_accepted[r] drafts accepted. ---- */
+ * n_draft[r] + 1), drafts[r][0..n_draft[r]), generated tokens so far
+ * generated[gen_off[r] .. gen_off[r+1]) (the penalties' and min_tokens' history; NULL =
+ * none).  Greedy rows use `acceptance`; rows with temperature > 0 use speculative sampling
+ * with 32-bit uniforms: uniforms[r][j][0] the accept test and [r][j][1] the sample draw of
+ * position j (row stride 2 * (draft_stride + 1)), or, when uniforms is NULL, the ones
+ * derived from (seed, counter[r]).  Outputs: n_emit[r] tokens in out_tokens[r][0 ..
+ * draft_stride] (row stride draft_stride + 1), kv_keep[r] positions of the verified block
+ * to keep, n_accepted[r] drafts accepted. ---- */
 int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* row_off,
               const int32_t* drafts, int32_t draft_stride, const int32_t* n_draft,
-              const mc_sampling* sp, const uint64_t* counter, int32_t acceptance,
+              const mc_sampling* sp, const int32_t* generated, const int64_t* gen_off,
+              const uint64_t* counter, const uint32_t* uniforms, int32_t acceptance,
               int32_t* out_tokens, int32_t* n_emit, int32_t* kv_keep, int32_t* n_accepted);
 
 /* ---- fused step: ContinuousBatchGenerator.next() -> speculativeNext()
@@ -201,9 +219,11 @@ int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* r
  * accept, roll back, append history; one host synchronisation.  out_tokens[row][K+1],
  * out_counts[row] tokens emitted, out_finish[row] 0 running / 1 stop (EOS) / 2 length;
  * finished rows are removed.  forced_accept (NULL = none) caps each row's accepted drafts
- * (stress workloads with a forced accept-length schedule). ---- */
-int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_tokens, int32_t* out_counts,
-            int32_t* out_finish);
+ * (stress workloads with a forced accept-length schedule).  uniforms (NULL = derived from
+ * each row's seed and step counter) supplies the draws of sampled rows as in mc_accept,
+ * uniforms[row][j][kind] with row stride 2 * (K + 1). ---- */
+int mc_step(mc_batch* b, const int32_t* forced_accept, const uint32_t* uniforms, int32_t* out_tokens,
+            int32_t* out_counts, int32_t* out_finish);
 /* SpeculativeDecodingStats accumulated by mc_step (Scheduler.swift:474-476). */
 int mc_batch_stats(mc_batch* b, mc_spec_stats* out);
 /* Widths of the warm-cache forwards issued so far (the reference tests' decode-call

@@ -51,7 +51,10 @@ class SpecConfig(C.Structure):
 class Sampling(C.Structure):
     _fields_ = [
         ("temperature", C.c_float), ("top_p", C.c_float), ("has_seed", C.c_int32), ("seed", C.c_uint64),
-        ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("reject_token", C.c_int32),
+        ("n_eos", C.c_int32), ("eos", C.c_int32 * 8), ("reject_token", C.c_int32), ("top_k", C.c_int32),
+        ("min_p", C.c_float), ("repetition_penalty", C.c_float), ("presence_penalty", C.c_float),
+        ("frequency_penalty", C.c_float), ("min_tokens", C.c_int32), ("n_bias", C.c_int32),
+        ("bias_token", C.c_int32 * 16), ("bias_value", C.c_float * 16),
     ]
 
 
@@ -101,8 +104,8 @@ def load(path: str = LIB_PATH):
         "mc_batch_history": (C.c_int, [P, I32, P, I32, P]),
         "mc_forward": (C.c_int, [P, I32, P, P, P, P]),
         "mc_ngram_propose": (C.c_int, [P, P, I32, I32, I32, P, I32, P, P]),
-        "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, I32, P, P, P, P]),
-        "mc_step": (C.c_int, [P, P, P, P, P]),
+        "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, P, P, P, I32, P, P, P, P]),
+        "mc_step": (C.c_int, [P, P, P, P, P, P]),
         "mc_batch_stats": (C.c_int, [P, P]),
         "mc_batch_call_widths": (C.c_int, [P, P, I32]),
         "mc_batch_set_profiling": (C.c_int, [P, I32]),
@@ -130,7 +133,10 @@ def _i32(x) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
 
 
-def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1) -> Sampling:
+def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1, top_k=0, min_p=0.0,
+                  repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0, min_tokens=0,
+                  logit_bias=None) -> Sampling:
+    """SamplingParameters (Sampling.swift:163-194) as the C ABI's mc_sampling."""
     sp = Sampling()
     sp.temperature = float(temperature)
     sp.top_p = float(top_p)
@@ -142,6 +148,19 @@ def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1
     for i, e in enumerate(eos):
         sp.eos[i] = int(e)
     sp.reject_token = int(reject_token)
+    sp.top_k = int(top_k)
+    sp.min_p = float(min_p)
+    sp.repetition_penalty = float(repetition_penalty)
+    sp.presence_penalty = float(presence_penalty)
+    sp.frequency_penalty = float(frequency_penalty)
+    sp.min_tokens = max(0, int(min_tokens))
+    bias = sorted((logit_bias or {}).items())
+    if len(bias) > 16:
+        raise ValueError("at most 16 logit bias entries")
+    sp.n_bias = len(bias)
+    for i, (t, b) in enumerate(bias):
+        sp.bias_token[i] = int(t)
+        sp.bias_value[i] = float(b)
     return sp
 
 
@@ -275,9 +294,15 @@ class Batch:
         _check(load().mc_forward(self.h, len(rows), _p(rows), _p(counts), _p(tokens), _p(lg)))
         return lg
 
-    def step(self, forced_accept=None):
+    def step(self, forced_accept=None, uniforms=None):
+        """One speculative step; uniforms [rows][K + 1][2] uint32 replaces the derived draws."""
         fa = _i32(forced_accept) if forced_accept is not None else None
-        _check(load().mc_step(self.h, _p(fa), _p(self._tok), _p(self._cnt), _p(self._fin)))
+        u = None
+        if uniforms is not None:
+            u = np.ascontiguousarray(uniforms, dtype=np.uint32)
+            if u.size != self._tok.size * 2:
+                raise ValueError("uniforms must hold rows * (K + 1) * 2 draws")
+        _check(load().mc_step(self.h, _p(fa), _p(u), _p(self._tok), _p(self._cnt), _p(self._fin)))
         return self._tok.copy(), self._cnt.copy(), self._fin.copy()
 
     def stats(self) -> dict:
@@ -318,8 +343,10 @@ def ngram_propose(histories, max_suffix: int, min_context: int, limits) -> list[
 
 
 def accept(logits_rows: list[np.ndarray], drafts: list[list[int]], samplings: list[Sampling], counters,
-           acceptance: int):
-    """GPU acceptance over host logits: row r has len(drafts[r]) + 1 logits rows."""
+           acceptance: int, generated=None, uniforms=None):
+    """GPU acceptance over host logits: row r has len(drafts[r]) + 1 logits rows;
+    generated[r] the row's generated tokens so far (penalties, min_tokens); uniforms[r] a
+    [len(drafts[r]) + 1][2] array of caller draws (None = derived from seed and counter)."""
     B = len(drafts)
     V = logits_rows[0].shape[1]
     stride = max(1, max(len(d) for d in drafts))
@@ -334,10 +361,22 @@ def accept(logits_rows: list[np.ndarray], drafts: list[list[int]], samplings: li
         nd[r] = len(d)
     sp = (Sampling * B)(*samplings)
     ctr = np.ascontiguousarray(counters, dtype=np.uint64)
+    gen = goff = None
+    if generated is not None:
+        goff = np.zeros(B + 1, dtype=np.int64)
+        for r in range(B):
+            goff[r + 1] = goff[r] + len(generated[r])
+        gen = _i32(np.concatenate([np.asarray(g, dtype=np.int32) for g in generated]) if goff[-1] else np.zeros(1))
+    u = None
+    if uniforms is not None:
+        u = np.zeros((B, stride + 1, 2), dtype=np.uint32)
+        for r in range(B):
+            ur = np.asarray(uniforms[r], dtype=np.uint32).reshape(-1, 2)
+            u[r, : len(ur)] = ur
     out = np.zeros((B, stride + 1), dtype=np.int32)
     n_emit = np.zeros(B, dtype=np.int32)
     keep = np.zeros(B, dtype=np.int32)
     nacc = np.zeros(B, dtype=np.int32)
-    _check(load().mc_accept(_p(lg), V, B, _p(off), _p(dr), stride, _p(nd), C.cast(sp, C.c_void_p), _p(ctr),
-                            acceptance, _p(out), _p(n_emit), _p(keep), _p(nacc)))
+    _check(load().mc_accept(_p(lg), V, B, _p(off), _p(dr), stride, _p(nd), C.cast(sp, C.c_void_p), _p(gen), _p(goff),
+                            _p(ctr), _p(u), acceptance, _p(out), _p(n_emit), _p(keep), _p(nacc)))
     return [out[r, : n_emit[r]].tolist() for r in range(B)], keep.tolist(), nacc.tolist()

@@ -430,6 +430,8 @@ struct mc_batch {
   std::vector<int32_t> kv_len_host;
   uint64_t unseeded = 0;
   bool forced_none = true;  // the device's forced accept-length schedule is all -1
+  bool uniforms_on = false; // the device reads caller uniforms
+  int32_t* gen_cnt = nullptr;  // [R][V] generated-token counts (rows with penalties)
   // profiling
   bool profiling = false;
   std::vector<hipEvent_t> ev;
@@ -447,7 +449,7 @@ static void batch_free(mc_batch* b) {
   if (b->graph_def) (void)hipGraphDestroy(b->graph_def);
   for (void* p : {(void*)b->kv_mem, (void*)b->rope_cos, (void*)b->rope_sin, (void*)b->x, (void*)b->qkv,
                   (void*)b->q, (void*)b->att, (void*)b->act, (void*)b->logits, (void*)b->gemv_part,
-                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, (void*)b->attn_cnt, b->scratch,
+                  (void*)b->gemv_cnt, (void*)b->ssq, (void*)b->amax, (void*)b->aw.part_o, (void*)b->aw.part_ml, (void*)b->attn_cnt, b->scratch, (void*)b->gen_cnt,
                   (void*)b->moe_xn, (void*)b->moe_logits, (void*)b->moe_act, (void*)b->moe_out, (void*)b->moe_i32,
                   (void*)b->moe_wts, (void*)b->xn})
     if (p) (void)hipFree(p);
@@ -590,6 +592,9 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
                o_rej = take(R), o_dr = take(RK), o_stok = take(Ms), o_srow = take(Ms),
                o_spos = take(Ms), o_rs0 = take(R), o_nv = take(R), o_qb = take(R), o_sct = take(RK),
                o_sca = take(RK), o_scr = take(RK), o_forced = take(R), o_stats = take(8),
+               o_topk = take(R), o_mpl = take(R), o_rp = take(R), o_pp = take(R), o_fp = take(R),
+               o_mint = take(R), o_nb = take(R), o_bt = take(16 * R), o_bv = take(16 * R), o_proc = take(R),
+               o_uni = take(2 * RK), o_useu = take(2),
                // what a step returns, contiguous so that one copy brings it to the host:
                // [RK tokens | R counts | R finish | R proposal lengths | R KV lengths]
                o_otok = take(RK + 4 * R), o_ocnt = o_otok + RK, o_ofin = o_ocnt + R, o_np = o_ofin + R,
@@ -608,6 +613,13 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   s.qbase = I32(o_qb); s.scan_tok = I32(o_sct); s.scan_acc = I32(o_sca); s.scan_res = I32(o_scr);
   s.forced = I32(o_forced); s.out_tok = I32(o_otok); s.out_cnt = I32(o_ocnt); s.out_fin = I32(o_ofin);
   s.stats = reinterpret_cast<unsigned long long*>(base + o_stats);
+  auto F32 = [&](size_t o) { return reinterpret_cast<float*>(base + o); };
+  s.top_k = I32(o_topk); s.min_p_log = F32(o_mpl); s.rep_pen = F32(o_rp); s.pres_pen = F32(o_pp);
+  s.freq_pen = F32(o_fp); s.min_tokens = I32(o_mint); s.n_bias = I32(o_nb); s.bias_tok = I32(o_bt);
+  s.bias_val = F32(o_bv); s.proc = I32(o_proc);
+  s.uniforms = reinterpret_cast<const uint32_t*>(base + o_uni); s.use_uniforms = I32(o_useu);
+  if ((rc = dev_zero(&b->gen_cnt, R * (size_t)V))) { batch_free(b); return rc; }
+  s.gen_cnt = b->gen_cnt;
   if (!m->fake) { s.amax = b->amax; s.amax_nt = m->head().NT; }
   // forced = -1 (none), reject = -1
   {
@@ -911,31 +923,91 @@ extern "C" int mc_forward(mc_batch* b, int32_t nrows, const int32_t* rows, const
 }
 
 // --------------------------- admission ------------------------------------
-static int set_row_sampling(mc_batch* b, int row, const mc_sampling* sp) {
+// Host image of one row's sampler options, validated (mc_sampling in include/mlxcat_hip.h).
+struct RowSampling {
+  float temp = 0.f, top_p = 0.f, inv_t = 0.f, min_p_log = -INFINITY, rp = 1.f, pp = 0.f, fp = 0.f;
+  int32_t top_k = 0, min_tokens = 0, n_bias = 0, proc = 0, n_eos = 0;
+  int32_t bias_tok[16] = {0};
+  float bias_val[16] = {0};
+  int32_t eos[8] = {0};
+};
+
+static int row_sampling(const mc_sampling* sp, int V, RowSampling* o) {
+  const float vals[] = {sp->temperature, sp->top_p, sp->min_p, sp->repetition_penalty, sp->presence_penalty,
+                        sp->frequency_penalty};
+  for (float v : vals)
+    if (!std::isfinite(v)) return fail(MC_E_INVALID, "sampling: non-finite parameter");
+  if (sp->temperature < 0.f || sp->top_k < 0 || sp->min_p < 0.f || sp->min_p > 1.f || sp->repetition_penalty < 0.f ||
+      sp->n_bias < 0 || sp->n_bias > 16)
+    return fail(MC_E_INVALID, "sampling: parameter out of range");
+  for (int i = 0; i < sp->n_bias; ++i)
+    if (!std::isfinite(sp->bias_value[i])) return fail(MC_E_INVALID, "sampling: non-finite logit bias");
+  o->temp = sp->temperature;
+  o->top_p = sp->top_p;
+  o->inv_t = sp->temperature != 0.0f ? 1.0f / sp->temperature : 0.0f;
+  o->top_k = sp->top_k;
+  o->min_p_log = sp->min_p > 0.0f ? logf(sp->min_p) : -INFINITY;
+  o->rp = sp->repetition_penalty == 0.0f ? 1.0f : sp->repetition_penalty;
+  o->pp = sp->presence_penalty;
+  o->fp = sp->frequency_penalty;
+  o->min_tokens = std::max(0, sp->min_tokens);
+  o->n_eos = std::max(0, std::min(8, sp->n_eos));
+  for (int i = 0; i < o->n_eos; ++i) o->eos[i] = sp->eos[i];
+  for (int i = 0; i < sp->n_bias; ++i)  // ids outside the vocabulary are ignored (Sampling.swift:698)
+    if (sp->bias_token[i] >= 0 && sp->bias_token[i] < V) {
+      o->bias_tok[o->n_bias] = sp->bias_token[i];
+      o->bias_val[o->n_bias++] = sp->bias_value[i];
+    }
+  o->proc = (o->n_bias > 0 ? 1 : 0) | (o->min_tokens > 0 && o->n_eos > 0 ? 2 : 0) |
+            (o->rp != 1.0f || o->pp != 0.0f || o->fp != 0.0f ? 4 : 0);
+  return MC_OK;
+}
+
+static int set_row_f32(mc_batch* b, float* arr, int row, float v) {
+  int32_t w;
+  memcpy(&w, &v, 4);
+  return upload_i32(b, reinterpret_cast<int32_t*>(arr) + row, &w, 1);
+}
+
+// Per-row sampler state; `counted` are the tokens generated so far (the penalties' counts).
+static int set_row_sampling(mc_batch* b, int row, const mc_sampling* sp, const int32_t* counted, int n_counted) {
   StepState& s = b->s;
-  const float t = sp->temperature;
-  const float inv = t != 0.0f ? 1.0f / t : 0.0f;
-  int32_t rowv[16];
+  RowSampling q;
   int rc;
-  memcpy(&rowv[0], &t, 4);
-  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.temp) + row, rowv, 1))) return rc;
-  memcpy(&rowv[0], &sp->top_p, 4);
-  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.top_p) + row, rowv, 1))) return rc;
-  memcpy(&rowv[0], &inv, 4);
-  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.inv_temp) + row, rowv, 1))) return rc;
+  if ((rc = row_sampling(sp, s.V, &q))) return rc;
+  if ((rc = set_row_f32(b, s.temp, row, q.temp))) return rc;
+  if ((rc = set_row_f32(b, s.top_p, row, q.top_p))) return rc;
+  if ((rc = set_row_f32(b, s.inv_temp, row, q.inv_t))) return rc;
   if ((rc = set_row_i32(b, s.has_seed, row, sp->has_seed ? 1 : 0))) return rc;
   // unseeded rows: a per-batch stream keyed by admission order (global seed 7)
   const uint64_t seed = sp->has_seed ? sp->seed : mix64(7ull ^ mix64(++b->unseeded));
-  uint64_t two[2] = {seed, 0};
+  int32_t rowv[4];
+  const uint64_t two[2] = {seed, 0};
   memcpy(rowv, two, 16);
   if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.seed + row), rowv, 2))) return rc;
   if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.counter + row), rowv + 2, 2))) return rc;
-  int32_t eos[8] = {0};
-  const int ne = std::max(0, std::min(8, sp->n_eos));
-  for (int i = 0; i < ne; ++i) eos[i] = sp->eos[i];
-  if ((rc = upload_i32(b, s.eos + row * 8, eos, 8))) return rc;
-  if ((rc = set_row_i32(b, s.n_eos, row, ne))) return rc;
-  return set_row_i32(b, s.reject, row, sp->reject_token);
+  if ((rc = upload_i32(b, s.eos + row * 8, q.eos, 8))) return rc;
+  if ((rc = set_row_i32(b, s.n_eos, row, q.n_eos))) return rc;
+  if ((rc = set_row_i32(b, s.reject, row, sp->reject_token))) return rc;
+  if ((rc = set_row_i32(b, s.top_k, row, q.top_k))) return rc;
+  if ((rc = set_row_f32(b, s.min_p_log, row, q.min_p_log))) return rc;
+  if ((rc = set_row_f32(b, s.rep_pen, row, q.rp))) return rc;
+  if ((rc = set_row_f32(b, s.pres_pen, row, q.pp))) return rc;
+  if ((rc = set_row_f32(b, s.freq_pen, row, q.fp))) return rc;
+  if ((rc = set_row_i32(b, s.min_tokens, row, q.min_tokens))) return rc;
+  if ((rc = set_row_i32(b, s.n_bias, row, q.n_bias))) return rc;
+  if ((rc = upload_i32(b, s.bias_tok + row * 16, q.bias_tok, 16))) return rc;
+  int32_t bv[16];
+  memcpy(bv, q.bias_val, sizeof bv);
+  if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(s.bias_val) + row * 16, bv, 16))) return rc;
+  if ((rc = set_row_i32(b, s.proc, row, q.proc))) return rc;
+  if (q.proc & 4) {  // the row's generated-token counts
+    std::vector<int32_t> c((size_t)s.V, 0);
+    for (int i = 0; i < n_counted; ++i)
+      if (counted[i] >= 0 && counted[i] < s.V) c[(size_t)counted[i]]++;
+    if ((rc = upload_i32(b, b->gen_cnt + (size_t)row * s.V, c.data(), c.size()))) return rc;
+  }
+  return MC_OK;
 }
 
 static int check_row(mc_batch* b, int row) {
@@ -983,7 +1055,7 @@ extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, 
   if ((rc = set_row_i32(b, s.cur, row, prompt[n_prompt - 1]))) return rc;
   if ((rc = set_row_i32(b, s.kv_len, row, n_prompt - 1))) return rc;
   if ((rc = set_row_i32(b, s.nprop, row, 0))) return rc;
-  if ((rc = set_row_sampling(b, row, sp))) return rc;
+  if ((rc = set_row_sampling(b, row, sp, nullptr, 0))) return rc;
   if ((rc = set_row_i32(b, s.active, row, 1))) return rc;
   if ((rc = launch_accept_scan(s, b->logits, row, b->st))) return rc;
   if ((rc = launch_commit(s, row, b->st))) return rc;
@@ -1029,7 +1101,8 @@ extern "C" int mc_batch_insert_prefilled(mc_batch* b, int32_t row, const int32_t
   if ((rc = set_row_i32(b, s.gen, row, 1))) return rc;
   if ((rc = set_row_i32(b, s.max_gen, row, max_tokens))) return rc;
   if ((rc = set_row_i32(b, s.cur, row, ctx[n_ctx - 1]))) return rc;
-  if ((rc = set_row_sampling(b, row, sp))) return rc;
+  // the current token counts as generated (generatedTokenHistory holds it)
+  if ((rc = set_row_sampling(b, row, sp, ctx + n_ctx - 1, 1))) return rc;
   return set_row_i32(b, s.active, row, 1);
 }
 
@@ -1134,12 +1207,23 @@ static int enqueue_step(mc_batch* b) {
   return launch_commit(s, -1, b->st);
 }
 
-extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, int32_t* out_tokens, int32_t* out_counts,
-                       int32_t* out_finish) {
+extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, const uint32_t* uniforms, int32_t* out_tokens,
+                       int32_t* out_counts, int32_t* out_finish) {
   if (!b) return fail(MC_E_INVALID, "null batch");
   MC_HIP(hipSetDevice(b->m->device));
   int rc;
   const int R = b->R, K1 = b->K1;
+  // caller uniforms (the captured step reads them through a device flag)
+  if (uniforms) {
+    if ((rc = upload_i32(b, reinterpret_cast<int32_t*>(const_cast<uint32_t*>(b->s.uniforms)),
+                         reinterpret_cast<const int32_t*>(uniforms), (size_t)2 * R * K1)))
+      return rc;
+  }
+  if ((uniforms != nullptr) != b->uniforms_on) {
+    const int32_t on = uniforms ? 1 : 0;
+    if ((rc = upload_i32(b, const_cast<int32_t*>(b->s.use_uniforms), &on, 1))) return rc;
+    b->uniforms_on = uniforms != nullptr;
+  }
   // forced accept-length schedule (or none)
   // (uploaded only when it differs from the all-none schedule already on the device)
   if (forced_accept || !b->forced_none) {
@@ -1279,10 +1363,12 @@ extern "C" int mc_ngram_propose(const int32_t* hist, const int64_t* hist_off, in
 
 extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* row_off,
                          const int32_t* drafts, int32_t draft_stride, const int32_t* n_draft, const mc_sampling* sp,
-                         const uint64_t* counter, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
+                         const int32_t* generated, const int64_t* gen_off, const uint64_t* counter,
+                         const uint32_t* uniforms, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
                          int32_t* kv_keep, int32_t* n_accepted) {
   if (!logits || !row_off || !n_draft || !sp || !counter || !out_tokens || !n_emit || !kv_keep || !n_accepted || B <= 0 ||
-      vocab <= 0 || row_off[0] != 0 || draft_stride < 0 || (!drafts && draft_stride > 0))
+      vocab <= 0 || row_off[0] != 0 || draft_stride < 0 || (!drafts && draft_stride > 0) ||
+      (generated && !gen_off))
     return fail(MC_E_INVALID, "mc_accept: bad argument");
   int K = 0;
   for (int r = 0; r < B; ++r) {
@@ -1292,39 +1378,72 @@ extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const
       const int32_t t = drafts[(size_t)r * draft_stride + j];
       if (t < 0 || t >= vocab) return fail(MC_E_INVALID, "mc_accept: draft token out of range");
     }
+    if (generated && (gen_off[r + 1] < gen_off[r] || gen_off[0] != 0))
+      return fail(MC_E_INVALID, "mc_accept: gen_off must be non-decreasing from 0");
     K = std::max(K, n_draft[r]);
   }
+  if (K + 1 > 257) return fail(MC_E_INVALID, "mc_accept: at most 256 drafts per row");
   MC_HIP(hipSetDevice(g_device));
   const int K1 = K + 1;
-  const size_t nl = (size_t)row_off[B];
   // device state laid out as a StepState with row r's logits at slots r*K1 + j
   StepState s;
   s.R = B; s.K = K; s.K1 = K1; s.V = vocab; s.acceptance = acceptance; s.hcap = 1;
   std::vector<int32_t> h_nprop((size_t)B), h_nv((size_t)B), h_rs0((size_t)B), h_act((size_t)B, 1), h_dr((size_t)B * K1, 0),
-      h_eos((size_t)B * 8, 0), h_neos((size_t)B), h_rej((size_t)B), h_hs((size_t)B), h_forced((size_t)B, -1);
-  std::vector<float> h_t((size_t)B), h_tp((size_t)B), h_it((size_t)B);
+      h_eos((size_t)B * 8, 0), h_neos((size_t)B), h_rej((size_t)B), h_hs((size_t)B), h_forced((size_t)B, -1),
+      h_topk((size_t)B), h_mint((size_t)B), h_nb((size_t)B), h_bt((size_t)B * 16, 0), h_proc((size_t)B), h_gen((size_t)B, 0),
+      h_useu(1, uniforms ? 1 : 0);
+  std::vector<float> h_t((size_t)B), h_tp((size_t)B), h_it((size_t)B), h_mpl((size_t)B), h_rp((size_t)B), h_pp((size_t)B),
+      h_fp((size_t)B), h_bv((size_t)B * 16, 0.f);
   std::vector<uint64_t> h_seed((size_t)B), h_ctr((size_t)B);
+  std::vector<uint32_t> h_uni(uniforms ? (size_t)B * K1 * 2 : 1, 0u);
+  bool any_pen = false;
   for (int r = 0; r < B; ++r) {
+    RowSampling q;
+    int rc0 = row_sampling(&sp[r], vocab, &q);
+    if (rc0) return rc0;
     h_nprop[(size_t)r] = n_draft[r];
     h_nv[(size_t)r] = n_draft[r] + 1;
     h_rs0[(size_t)r] = r * K1;
     for (int j = 0; j < n_draft[r]; ++j) h_dr[(size_t)r * K1 + j] = drafts[(size_t)r * draft_stride + j];
-    const auto& q = sp[r];
-    h_t[(size_t)r] = q.temperature;
+    h_t[(size_t)r] = q.temp;
     h_tp[(size_t)r] = q.top_p;
-    h_it[(size_t)r] = q.temperature != 0.0f ? 1.0f / q.temperature : 0.0f;
-    h_hs[(size_t)r] = q.has_seed;
-    h_seed[(size_t)r] = q.seed;
+    h_it[(size_t)r] = q.inv_t;
+    h_hs[(size_t)r] = sp[r].has_seed;
+    h_seed[(size_t)r] = sp[r].seed;
     h_ctr[(size_t)r] = counter[r];
-    const int ne = std::max(0, std::min(8, q.n_eos));
-    for (int i = 0; i < ne; ++i) h_eos[(size_t)r * 8 + i] = q.eos[i];
-    h_neos[(size_t)r] = ne;
-    h_rej[(size_t)r] = q.reject_token;
+    for (int i = 0; i < q.n_eos; ++i) h_eos[(size_t)r * 8 + i] = q.eos[i];
+    h_neos[(size_t)r] = q.n_eos;
+    h_rej[(size_t)r] = sp[r].reject_token;
+    h_topk[(size_t)r] = q.top_k;
+    h_mpl[(size_t)r] = q.min_p_log;
+    h_rp[(size_t)r] = q.rp;
+    h_pp[(size_t)r] = q.pp;
+    h_fp[(size_t)r] = q.fp;
+    h_mint[(size_t)r] = q.min_tokens;
+    h_nb[(size_t)r] = q.n_bias;
+    for (int i = 0; i < 16; ++i) {
+      h_bt[(size_t)r * 16 + i] = q.bias_tok[i];
+      h_bv[(size_t)r * 16 + i] = q.bias_val[i];
+    }
+    h_proc[(size_t)r] = q.proc;
+    any_pen = any_pen || (q.proc & 4);
+    h_gen[(size_t)r] = generated ? (int32_t)(gen_off[r + 1] - gen_off[r]) : 0;
+    if (uniforms)
+      for (int j = 0; j <= n_draft[r]; ++j)
+        for (int k = 0; k < 2; ++k)
+          h_uni[((size_t)r * K1 + j) * 2 + k] = uniforms[((size_t)r * (draft_stride + 1) + j) * 2 + k];
   }
+  // generated-token counts of the rows with penalties
+  std::vector<int32_t> h_cnt(any_pen ? (size_t)B * vocab : 1, 0);
+  if (any_pen && generated)
+    for (int r = 0; r < B; ++r) {
+      if (!(h_proc[(size_t)r] & 4)) continue;
+      for (int64_t i = gen_off[r]; i < gen_off[r + 1]; ++i)
+        if (generated[i] >= 0 && generated[i] < vocab) h_cnt[(size_t)r * vocab + generated[i]]++;
+    }
   std::vector<uint16_t> h_lg((size_t)B * K1 * vocab, 0);
   for (int r = 0; r < B; ++r)
     memcpy(&h_lg[(size_t)r * K1 * vocab], logits + (size_t)row_off[r] * vocab, (size_t)(n_draft[r] + 1) * vocab * 2);
-  (void)nl;
   std::vector<void*> allocs;
   int rc = MC_OK;
   auto up = [&](auto** dst, const auto& src) -> int {
@@ -1356,6 +1475,26 @@ extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const
   if (!rc) rc = up(&s.n_eos, h_neos);
   if (!rc) rc = up(&s.reject, h_rej);
   if (!rc) rc = up(&s.forced, h_forced);
+  if (!rc) rc = up(&s.top_k, h_topk);
+  if (!rc) rc = up(&s.min_p_log, h_mpl);
+  if (!rc) rc = up(&s.rep_pen, h_rp);
+  if (!rc) rc = up(&s.pres_pen, h_pp);
+  if (!rc) rc = up(&s.freq_pen, h_fp);
+  if (!rc) rc = up(&s.min_tokens, h_mint);
+  if (!rc) rc = up(&s.n_bias, h_nb);
+  if (!rc) rc = up(&s.bias_tok, h_bt);
+  if (!rc) rc = up(&s.bias_val, h_bv);
+  if (!rc) rc = up(&s.proc, h_proc);
+  if (!rc) rc = up(&s.gen, h_gen);
+  if (!rc) rc = up(&s.gen_cnt, h_cnt);
+  {
+    uint32_t* du = nullptr;
+    int32_t* df = nullptr;
+    if (!rc) rc = up(&du, h_uni);
+    if (!rc) rc = up(&df, h_useu);
+    s.uniforms = du;
+    s.use_uniforms = df;
+  }
   if (!rc) rc = up(&s.scan_tok, zeros_rk);
   if (!rc) rc = up(&s.scan_acc, zeros_rk);
   if (!rc) rc = up(&s.scan_res, zeros_rk);

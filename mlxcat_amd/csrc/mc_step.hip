@@ -8,11 +8,13 @@
 //             lexicographic maximum of (min(l(e), n - e), e) over candidate ends e, where
 //             l(e) is the backward match length at e; one block computes every l(e) in
 //             parallel and max-reduces the packed key.
-//   scan:     per (row, verify position): greedy argmax (lowest index on ties), or the
-//             integer-mass target distribution of a sampled row (top-p as
-//             Sampling.swift:847-858 on T=1 masses, then temperature), the accept test
-//             of the draft token (u < p(x), one-hot n-gram draft) and the residual /
-//             bonus sample.
+//   scan:     per (row, verify position): the values the position samples from (the
+//             logits, or with logit bias / min_tokens / penalties the processed fp32
+//             values of Sampling.swift:592-652), then greedy argmax (lowest index on
+//             ties), or the integer-mass target distribution of a sampled row (top-p as
+//             Sampling.swift:847-858 on T=1 masses, min-p, top-k, then temperature), the
+//             accept test of the draft token (u < p(x), one-hot n-gram draft) and the
+//             residual / bonus sample.
 //   commit:   per row: the acceptance rule (the reference's all-or-nothing loop
 //             :906-947, or longest-prefix / speculative sampling), KV rollback by length,
 //             history append (:1012-1014), stats (:894-895,938,952) and finish reasons
@@ -133,11 +135,10 @@ int launch_ngram_standalone(const int32_t* hist, const int64_t* off, int B, int 
 // ---------------------------------------------------------------------------
 constexpr int SCAN_THREADS = 1024;
 
-__device__ inline float canon_bf16(uint16_t h) { return (h & 0x7FFFu) == 0 ? 0.0f : bf16_to_f32(h); }
-// order-preserving 16-bit key of a bf16 value (with -0 folded into +0)
-__device__ inline uint32_t key16(uint16_t h) {
-  if ((h & 0x7FFFu) == 0) h = 0;
-  return (h & 0x8000u) ? (uint32_t)(~h & 0xFFFFu) : (uint32_t)(h | 0x8000u);
+// order-preserving 32-bit key of an fp32 value (callers fold -0 into +0 first)
+__device__ inline uint32_t key32(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 // floor(u * T / 2^32) for u < 2^32, T < 2^60
 __device__ inline uint64_t mulhi32(uint32_t u, uint64_t T) {
@@ -157,6 +158,24 @@ __device__ inline uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
   __syncthreads();
   return t;
+}
+
+// exclusive prefix sum over the block's threads in thread order
+__device__ inline uint64_t block_excl_scan_u64(uint64_t v, uint64_t* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = (uint64_t)__shfl_up((unsigned long long)x, o);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  uint64_t off = 0;
+  for (int i = 0; i < w; ++i) off += red[i];
+  __syncthreads();
+  return off + x - v;
 }
 
 __device__ inline unsigned long long block_max_u64(unsigned long long v, uint64_t* red) {
@@ -188,13 +207,52 @@ __device__ inline float block_max_f(float v, float* red) {
   return t;
 }
 
+// The values one (row, position) samples from: the bf16 logits in fp32, and for rows with
+// logits processors or penalties (Sampling.swift:638-652, 592-636) the logit bias, the
+// min_tokens EOS mask and the repetition / presence / frequency penalties over the
+// generated tokens (the row's, then the drafts before this position).  -0 reads as +0.
+struct PosVals {
+  const uint16_t* lg = nullptr;
+  int proc = 0;
+  int nb = 0;                 // bias entries
+  const int32_t* bt = nullptr;
+  const float* bv = nullptr;
+  int ne = 0;                 // EOS ids to mask (0 = no mask at this position)
+  const int32_t* eos = nullptr;
+  int pen = 0;
+  float rp = 1.f, pp = 0.f, fp = 0.f;
+  const int32_t* cnt = nullptr;  // [V] generated-token counts of the row
+  const int32_t* dr = nullptr;   // drafts before this position
+  int nd = 0;
+  __device__ float operator()(int i) const {
+#pragma clang fp contract(off)
+    float v = bf16_to_f32(lg[i]);
+    if (proc) {
+      for (int k = 0; k < nb; ++k)
+        if (bt[k] == i) v = v + bv[k];
+      for (int k = 0; k < ne; ++k)
+        if (eos[k] == i) v = -INFINITY;
+      if (pen) {
+        int c = cnt[i];
+        for (int t = 0; t < nd; ++t) c += dr[t] == i;
+        if (c > 0) {
+          if (rp != 1.0f) v = v < 0.0f ? v * rp : v / rp;
+          if (pp != 0.0f) v = v - pp;
+          if (fp != 0.0f) v = v - (float)c * fp;
+        }
+      }
+    }
+    return v == 0.0f ? 0.0f : v;
+  }
+};
+
 // argmax with the lowest index on ties
-__device__ int block_argmax(const uint16_t* lg, int V, float* redv, int* redi) {
+__device__ int block_argmax(const PosVals& pv, int V, float* redv, int* redi) {
   const int tid = threadIdx.x;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
   for (int i = tid; i < V; i += blockDim.x) {
-    const float v = bf16_to_f32(lg[i]);
+    const float v = pv(i);
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
   }
 #pragma unroll
@@ -214,143 +272,226 @@ __device__ int block_argmax(const uint16_t* lg, int V, float* redv, int* redi) {
   return idx == 0x7FFFFFFF ? 0 : idx;
 }
 
+// Kept set and temperature mass total of one position (filters in the order of
+// Sampling.swift:500-522): top-p keeps key32(v) >= kstar, min-p keeps v - m >= lmp, top-k
+// keeps the top_k largest values, the lowest indices first among equal values.
 struct DistDev {
-  float m;          // max logit
-  uint32_t kstar;   // smallest kept key (0 = all kept)
+  float m;          // max value
+  uint32_t kstar;   // smallest kept key under top-p (0 = all kept)
+  float lmp;        // log(min_p), -inf = off
+  int has_k;
+  int ksh;          // top-k compares key32 >> ksh
+  uint32_t kk;      // ... against the k-th largest
+  int kidx;         // largest kept index among keys equal to kk
   uint64_t total;   // kept temperature mass
 };
 
-__device__ inline uint64_t tmass(const DistDev& d, uint16_t h, float inv_t) {
+__device__ inline bool dkept(const DistDev& d, float v, int i) {
 #pragma clang fp contract(off)
-  if (key16(h) < d.kstar) return 0;
-  const float v = canon_bf16(h);
+  const uint32_t k = key32(v);
+  if (k < d.kstar) return false;
+  if (!(v - d.m >= d.lmp)) return false;
+  if (d.has_k) {
+    const uint32_t kt = k >> d.ksh;
+    if (kt < d.kk || (kt == d.kk && i > d.kidx)) return false;
+  }
+  return true;
+}
+
+__device__ inline uint64_t tmass(const DistDev& d, float v, int i, float inv_t) {
+#pragma clang fp contract(off)
+  if (!dkept(d, v, i)) return 0;
   return mass_of(exp_neg_det((v - d.m) * inv_t));
 }
 
-__device__ DistDev dist_build_dev(const uint16_t* lg, int V, float inv_t, float top_p, uint64_t* hist, uint64_t* red,
-                                  float* redf, int* s_int, uint64_t* s_u64) {
+// Radix selection over `nlev` 8-bit digits of the keys (2 for plain bf16 values, whose keys'
+// low 16 bits carry nothing, 4 for processed fp32 values).
+__device__ DistDev dist_build_dev(const PosVals& pv, int V, float inv_t, float top_p, int top_k, float lmp, int nlev,
+                                  uint64_t* hist, uint64_t* red, float* redf, int* s_int, uint64_t* s_u64) {
 #pragma clang fp contract(off)
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nt = blockDim.x;
   DistDev d;
   float mx = -INFINITY;
-  for (int i = tid; i < V; i += blockDim.x) mx = fmaxf(mx, canon_bf16(lg[i]));
+  for (int i = tid; i < V; i += nt) mx = fmaxf(mx, pv(i));
   d.m = block_max_f(mx, redf);
   d.kstar = 0;
+  d.lmp = lmp;
   if (top_p > 0.0f && top_p < 1.0f) {
-    for (int i = tid; i < 512; i += blockDim.x) hist[i] = 0;
-    __syncthreads();
-    uint64_t t1 = 0;
-    for (int i = tid; i < V; i += blockDim.x) {
-      const uint16_t h = lg[i];
-      const uint64_t w = mass_of(exp_neg_det(canon_bf16(h) - d.m));
-      t1 += w;
-      if (w) atomicAdd((unsigned long long*)&hist[key16(h) >> 8], (unsigned long long)w);
-    }
-    const uint64_t total1 = block_sum_u64(t1, red);
-    const double X = (double)top_p * (double)total1;
-    if (tid == 0) {
-      uint64_t cum = 0, base = 0;
-      int hb = -1;
-      for (int b = 255; b >= 0; --b) {
-        if (hist[b] == 0) continue;
-        if (!((double)cum < X)) break;
-        hb = b;
-        base = cum;
-        cum += hist[b];
+    // Sampling.swift:847-858 on T=1 masses: the kept values are those >= the smallest value
+    // whose strictly-larger values hold less than top_p of the mass
+    uint32_t prefix = 0;
+    uint64_t base = 0;
+    double X = 0.0;
+    bool ok = true;
+    for (int lev = 0; lev < nlev; ++lev) {
+      const int sh = 24 - 8 * lev;
+      for (int b = tid; b < 256; b += nt) hist[b] = 0;
+      __syncthreads();
+      uint64_t t1 = 0;
+      for (int i = tid; i < V; i += nt) {
+        const float v = pv(i);
+        const uint32_t k = key32(v);
+        if (lev > 0 && (k >> (sh + 8)) != prefix) continue;
+        const uint64_t w = mass_of(exp_neg_det(v - d.m));
+        t1 += w;
+        if (w) atomicAdd((unsigned long long*)&hist[(k >> sh) & 255u], (unsigned long long)w);
       }
-      s_int[0] = hb;
-      s_u64[0] = base;
-    }
-    __syncthreads();
-    const int hb = s_int[0];
-    for (int i = tid; i < V; i += blockDim.x) {
-      const uint16_t h = lg[i];
-      const uint32_t k = key16(h);
-      if ((int)(k >> 8) != hb) continue;
-      const uint64_t w = mass_of(exp_neg_det(canon_bf16(h) - d.m));
-      if (w) atomicAdd((unsigned long long*)&hist[256 + (k & 255u)], (unsigned long long)w);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t cum = s_u64[0];
-      int lo = -1;
-      for (int b = 255; b >= 0; --b) {
-        if (hist[256 + b] == 0) continue;
-        if (!((double)cum < X)) break;
-        lo = b;
-        cum += hist[256 + b];
+      if (lev == 0)
+        X = (double)top_p * (double)block_sum_u64(t1, red);
+      else
+        __syncthreads();
+      if (tid == 0) {
+        uint64_t cum = base, sb = base;
+        int sel = -1;
+        for (int b = 255; b >= 0; --b) {
+          if (hist[b] == 0) continue;
+          if (!((double)cum < X)) break;
+          sel = b;
+          sb = cum;
+          cum += hist[b];
+        }
+        s_int[0] = sel;
+        s_u64[0] = sb;
       }
-      // hb >= 0 and lo >= 0 whenever the row has a finite maximum
-      s_int[1] = (hb < 0 || lo < 0) ? 0 : ((hb << 8) | lo);
+      __syncthreads();
+      const int sel = s_int[0];
+      base = s_u64[0];
+      __syncthreads();
+      if (sel < 0) { ok = false; break; }  // block-uniform
+      prefix = (prefix << 8) | (uint32_t)sel;
+    }
+    d.kstar = ok ? prefix << (32 - 8 * nlev) : 0u;
+  }
+  d.has_k = top_k > 0 && top_k < V;
+  d.ksh = 32 - 8 * nlev;
+  d.kk = 0;
+  d.kidx = 0x7FFFFFFF;
+  if (d.has_k) {
+    // Sampling.swift:893-906: the top_k-th largest key, then the index cutoff among its ties
+    unsigned* cnt = reinterpret_cast<unsigned*>(hist);
+    uint32_t prefix = 0;
+    int need = top_k;
+    for (int lev = 0; lev < nlev; ++lev) {
+      const int sh = 24 - 8 * lev;
+      for (int b = tid; b < 256; b += nt) cnt[b] = 0u;
+      __syncthreads();
+      for (int i = tid; i < V; i += nt) {
+        const uint32_t k = key32(pv(i));
+        if (lev > 0 && (k >> (sh + 8)) != prefix) continue;
+        atomicAdd(&cnt[(k >> sh) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int cum = 0, sel = 0;
+        for (int b = 255; b >= 0; --b) {
+          if (cum + (int)cnt[b] >= need) { sel = b; break; }
+          cum += (int)cnt[b];
+        }
+        s_int[1] = sel;
+        s_int[2] = need - cum;
+      }
+      __syncthreads();
+      prefix = (prefix << 8) | (uint32_t)s_int[1];
+      need = s_int[2];
+      __syncthreads();
+    }
+    d.kk = prefix;
+    const int chunk = (V + nt - 1) / nt;
+    const int b0 = min(V, tid * chunk), b1 = min(V, b0 + chunk);
+    int c = 0;
+    for (int i = b0; i < b1; ++i) c += (key32(pv(i)) >> d.ksh) == prefix;
+    if (tid == 0) s_int[3] = 0x7FFFFFFF;
+    const int start = (int)block_excl_scan_u64((uint64_t)c, red);
+    if (start < need && need <= start + c) {
+      int seen = start;
+      for (int i = b0; i < b1; ++i)
+        if ((key32(pv(i)) >> d.ksh) == prefix && ++seen == need) { s_int[3] = i; break; }
     }
     __syncthreads();
-    d.kstar = (uint32_t)s_int[1];
+    d.kidx = s_int[3];
+    __syncthreads();
   }
   uint64_t tt = 0;
-  for (int i = tid; i < V; i += blockDim.x) tt += tmass(d, lg[i], inv_t);
+  for (int i = tid; i < V; i += nt) tt += tmass(d, pv(i), i, inv_t);
   d.total = block_sum_u64(tt, red);
   return d;
 }
 
 // index-order inverse-CDF sample of floor(u * total' / 2^32), total' excluding `ex`
-__device__ int dist_sample_dev(const DistDev& d, const uint16_t* lg, int V, float inv_t, uint32_t u, int ex,
-                               uint64_t wx, uint64_t* scan, int* s_int) {
+__device__ int dist_sample_dev(const DistDev& d, const PosVals& pv, int V, float inv_t, uint32_t u, int ex,
+                               uint64_t wx, uint64_t* red, int* s_int) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const uint64_t total = d.total - (ex >= 0 ? wx : 0);
   const uint64_t R = mulhi32(u, total);
   const int chunk = (V + nt - 1) / nt;
-  const int b0 = tid * chunk, b1 = min(V, b0 + chunk);
+  const int b0 = min(V, tid * chunk), b1 = min(V, b0 + chunk);
   uint64_t cs = 0;
   for (int i = b0; i < b1; ++i)
-    if (i != ex) cs += tmass(d, lg[i], inv_t);
-  scan[tid] = cs;
-  if (tid == 0) s_int[2] = -1;
-  __syncthreads();
-  // exclusive prefix over threads (sequential per wave leader; 16 waves)
-  if (tid == 0) {
-    uint64_t acc = 0;
-    for (int i = 0; i < nt; ++i) {
-      const uint64_t v = scan[i];
-      scan[i] = acc;
-      acc += v;
-    }
-  }
-  __syncthreads();
-  const uint64_t start = scan[tid];
+    if (i != ex) cs += tmass(d, pv(i), i, inv_t);
+  if (tid == 0) s_int[4] = -1;
+  const uint64_t start = block_excl_scan_u64(cs, red);
   if (R >= start && R < start + cs) {
     uint64_t c = start;
     for (int i = b0; i < b1; ++i) {
       if (i == ex) continue;
-      const uint64_t w = tmass(d, lg[i], inv_t);
+      const uint64_t w = tmass(d, pv(i), i, inv_t);
       if (w == 0) continue;
-      if (c + w > R) { s_int[2] = i; break; }
+      if (c + w > R) { s_int[4] = i; break; }
       c += w;
     }
   }
   __syncthreads();
-  const int tok = s_int[2];
+  const int tok = s_int[4];
   __syncthreads();
   return tok < 0 ? 0 : tok;
 }
 
 __global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, const uint16_t* logits, int row_filter) {
-  __shared__ uint64_t hist[512];
-  __shared__ uint64_t scan[SCAN_THREADS];
+  __shared__ uint64_t hist[256];
   __shared__ uint64_t red[16];
   __shared__ float redf[16];
   __shared__ int redi[16];
-  __shared__ int s_int[4];
+  __shared__ int s_int[8];
   __shared__ uint64_t s_u64[2];
+  __shared__ int32_t l_bt[16], l_eos[8], l_dr[256];
+  __shared__ float l_bv[16];
   const int r = blockIdx.x, j = blockIdx.y;
   if (row_filter >= 0 && r != row_filter) return;
   if (!s.active[r] || j >= s.n_valid[r]) return;
   const int P = s.nprop[r];
   const int slot = s.row_slot0[r] + j;
-  const uint16_t* lg = logits + (size_t)slot * s.V;
   const int V = s.V;
+  PosVals pv;
+  pv.lg = logits + (size_t)slot * V;
+  {
+    const int flags = s.proc ? s.proc[r] : 0;
+    pv.nb = (flags & 1) ? s.n_bias[r] : 0;
+    pv.ne = ((flags & 2) && s.gen[r] + j < s.min_tokens[r]) ? s.n_eos[r] : 0;
+    pv.pen = (flags & 4) ? 1 : 0;
+    pv.proc = pv.nb > 0 || pv.ne > 0 || pv.pen;
+  }
+  if (pv.proc) {  // block-uniform
+    const int tid = threadIdx.x;
+    if (tid < pv.nb) {
+      l_bt[tid] = s.bias_tok[r * 16 + tid];
+      l_bv[tid] = s.bias_val[r * 16 + tid];
+    }
+    if (tid < pv.ne) l_eos[tid] = s.eos[r * 8 + tid];
+    if (pv.pen && tid < j) l_dr[tid] = s.drafts[r * s.K1 + tid];
+    __syncthreads();
+    pv.bt = l_bt;
+    pv.bv = l_bv;
+    pv.eos = l_eos;
+    pv.dr = l_dr;
+    pv.nd = pv.pen ? j : 0;
+    pv.rp = s.rep_pen[r];
+    pv.pp = s.pres_pen[r];
+    pv.fp = s.freq_pen[r];
+    pv.cnt = s.gen_cnt + (size_t)r * V;
+  }
   if (s.temp[r] == 0.0f) {
     int t;
-    if (s.amax) {
+    if (s.amax && !pv.proc) {
       // max over the head's per-tile partials (value key << 32 | 0xFFFFFFFF - index)
       const unsigned long long* ap = s.amax + (size_t)slot * s.amax_nt;
       unsigned long long best = 0ull;
@@ -358,31 +499,36 @@ __global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, 
       best = block_max_u64(best, red);
       t = (int)(0xFFFFFFFFull - (best & 0xFFFFFFFFull));
     } else {
-      t = block_argmax(lg, V, redf, redi);
+      t = block_argmax(pv, V, redf, redi);
     }
     if (threadIdx.x == 0) s.scan_tok[r * s.K1 + j] = t;
     return;
   }
   const float inv_t = s.inv_temp[r];
-  const DistDev d = dist_build_dev(lg, V, inv_t, s.top_p[r], hist, red, redf, s_int, s_u64);
+  const DistDev d = dist_build_dev(pv, V, inv_t, s.top_p[r], s.top_k[r], s.min_p_log[r], pv.proc ? 4 : 2, hist, red,
+                                   redf, s_int, s_u64);
   const uint64_t seed = s.seed[r], ctr = s.counter[r];
+  const bool caller_u = s.use_uniforms && *s.use_uniforms;
+  const uint32_t* uu = caller_u ? s.uniforms + ((size_t)r * s.K1 + j) * 2 : nullptr;
+  const uint32_t u_acc = caller_u ? uu[0] : uniform_u32(seed, ctr, (uint32_t)j, 0u);
+  const uint32_t u_smp = caller_u ? uu[1] : uniform_u32(seed, ctr, (uint32_t)j, 1u);
   if (j < P) {
     const int x = s.drafts[r * s.K1 + j];
-    const uint64_t wx = tmass(d, lg[x], inv_t);
-    const uint32_t u0 = uniform_u32(seed, ctr, (uint32_t)j, 0u);
-    const int acc = mulhi32(u0, d.total) < wx;
-    const int res = dist_sample_dev(d, lg, V, inv_t, uniform_u32(seed, ctr, (uint32_t)j, 1u), x, wx, scan, s_int);
+    const uint64_t wx = tmass(d, pv(x), x, inv_t);
+    const int acc = mulhi32(u_acc, d.total) < wx;
+    const int res = dist_sample_dev(d, pv, V, inv_t, u_smp, x, wx, red, s_int);
     if (threadIdx.x == 0) {
       s.scan_acc[r * s.K1 + j] = acc;
       s.scan_res[r * s.K1 + j] = res;
     }
   } else {
-    const int res = dist_sample_dev(d, lg, V, inv_t, uniform_u32(seed, ctr, (uint32_t)j, 1u), -1, 0, scan, s_int);
+    const int res = dist_sample_dev(d, pv, V, inv_t, u_smp, -1, 0, red, s_int);
     if (threadIdx.x == 0) s.scan_res[r * s.K1 + j] = res;
   }
 }
 
 int launch_accept_scan(const StepState& s, const uint16_t* logits, int row_filter, hipStream_t st) {
+  if (s.K1 > 257) return fail(MC_E_INVALID, "accept scan: K too large");
   hipLaunchKernelGGL(accept_scan_kernel, dim3(s.R, s.K1), dim3(SCAN_THREADS), 0, st, s, logits, row_filter);
   MC_HIP(hipGetLastError());
   return MC_OK;
@@ -486,9 +632,11 @@ __global__ void commit_kernel(StepState s, int row_filter) {
   s.kv_len[r] = s.qbase[r] + keep;  // rollback: keep current token + accepted drafts
   int fin = 0, emitted = 0;
   int32_t* h = s.hist + (size_t)r * s.hcap;
+  int32_t* cnt = (s.proc && (s.proc[r] & 4)) ? s.gen_cnt + (size_t)r * s.V : nullptr;
   for (int z = 0; z < n; ++z) {
     const int t = out[z];
     if (s.hist_len[r] < s.hcap) h[s.hist_len[r]++] = t;
+    if (cnt) cnt[t] += 1;  // the penalties' token counts
     s.gen[r] += 1;
     ++emitted;
     fin = is_eos(s, r, t) ? 1 : (s.gen[r] >= s.max_gen[r] ? 2 : 0);

@@ -29,6 +29,22 @@ struct StepState {
   int32_t* eos = nullptr;       // [R][8]
   int32_t* n_eos = nullptr;
   int32_t* reject = nullptr;
+  // sampler options beyond temperature / top-p (Sampling.swift:139-217)
+  int32_t* top_k = nullptr;     // 0 = off
+  float* min_p_log = nullptr;   // log(min_p), -inf = off
+  float* rep_pen = nullptr;     // 1 = off
+  float* pres_pen = nullptr;
+  float* freq_pen = nullptr;
+  int32_t* min_tokens = nullptr;
+  int32_t* n_bias = nullptr;
+  int32_t* bias_tok = nullptr;  // [R][16]
+  float* bias_val = nullptr;    // [R][16]
+  int32_t* proc = nullptr;      // bit 0: bias, bit 1: min_tokens mask possible, bit 2: penalties
+  int32_t* gen_cnt = nullptr;   // [R][V] occurrences of each token among the generated ones
+                                // (maintained for rows with penalties only)
+  // caller-supplied uniforms [R][K1][2] (accept test, sample draw), used when *use_uniforms
+  const uint32_t* uniforms = nullptr;
+  const int32_t* use_uniforms = nullptr;
   // step scratch
   int32_t* drafts = nullptr;    // [R][K1]
   int32_t* nprop = nullptr;     // [R]

@@ -77,15 +77,27 @@ class Response:
 
 @dataclass
 class SamplingParameters:
+    """SamplingParameters (Sampling.swift:139-194) minus the grammar, XTC and thinking-budget
+    options, which the step does not implement."""
     temperature: float = 0.0
     top_p: float = 0.0
+    top_k: int = 0
+    min_p: float = 0.0
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+    min_tokens: int = 0
+    logit_bias: dict = field(default_factory=dict)
     seed: int | None = None
     eos_token_ids: tuple = ()
     tool_call_start_token_id: int | None = None
 
     def as_c(self) -> L.Sampling:
         return L.make_sampling(self.temperature, self.top_p, self.seed, tuple(self.eos_token_ids),
-                               -1 if self.tool_call_start_token_id is None else self.tool_call_start_token_id)
+                               -1 if self.tool_call_start_token_id is None else self.tool_call_start_token_id,
+                               top_k=self.top_k, min_p=self.min_p, repetition_penalty=self.repetition_penalty,
+                               presence_penalty=self.presence_penalty, frequency_penalty=self.frequency_penalty,
+                               min_tokens=self.min_tokens, logit_bias=self.logit_bias)
 
 
 _FIN = {0: None, 1: FinishReason.STOP, 2: FinishReason.LENGTH}

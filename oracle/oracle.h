@@ -13,7 +13,9 @@
  *      tool-trigger reject, stats at :894-895,938,952)
  *   - step gate            BatchGenerator.swift:957-980
  *   - finish reasons       Sources/MLXCat/TrackB/Scheduler.swift:372-401,1215-1227
- *   - top-p filter         Sources/MLXCat/TrackB/Sampling.swift:847-858
+ *   - sampler              Sources/MLXCat/TrackB/Sampling.swift:483-528,592-652,847-906
+ *     (logit bias, minTokens EOS mask, repetition / presence / frequency penalties,
+ *      top-p, min-p, top-k, temperature)
  *   - KV trim              Sources/MLXCat/TrackB/BatchCache.swift:403-424
  *   - 4-bit affine g64 group cost  Sources/MLXCat/TrackB/KVQuantizationPolicy.swift:12-14
  * Beyond the reference (it speculates only at width 1, greedy): batched
@@ -78,34 +80,60 @@ int or_ngram_propose(const int32_t* ctx, int n, int max_suffix, int min_context,
 /* ---- acceptance building blocks ---- */
 /* argmax over bf16 logits, lowest index wins ties (MLX argMax convention) */
 int or_argmax_bf16(const uint16_t* logits, int V);
-/* Integer-mass sampling state of one logits row.  top_p in (0,1) filters with
- * Sampling.swift:847-858 semantics on T=1 masses; temperature scales the kept
- * logits.  Masses are round(exp(.) * 2^32) as uint64. */
+/* Integer-mass sampling state of one position's values (the fp32 logits after the
+ * processors and penalties of or_process_logits).  Filters, in the order of
+ * Sampling.swift:500-522: top-p in (0,1) with :847-858 semantics on T=1 masses, min-p
+ * (:860-863: keep v - max >= log(min_p)), top-k (:893-906: the k largest values, the
+ * lowest indices first among equal values); the temperature then scales the kept values.
+ * Masses are round(exp(.) * 2^32) as uint64. */
 typedef struct or_dist {
   uint64_t total;     /* sum of kept temperature masses */
   float max_logit;
-  float tau;          /* smallest kept logit value (top-p threshold) */
+  float tau;          /* smallest kept value under top-p */
   int filtered;       /* 1 if top-p was applied */
+  float min_p_log;    /* log(min_p); -inf when min-p is off */
+  float topk_value;   /* the k-th largest value; -inf when top-k is off */
+  int32_t topk_index; /* among values equal to topk_value, larger indices are dropped */
 } or_dist;
+struct or_sampling;
+void or_dist_build_f(const float* v, int V, float temperature, float top_p, int top_k, float min_p_log,
+                     or_dist* d);
+uint64_t or_dist_mass_f(const or_dist* d, const float* v, float inv_temp, int token);
+/* sample with 32-bit uniform u from the kept distribution, excluding `exclude` (-1: none) */
+int or_dist_sample_f(const or_dist* d, const float* v, int V, float inv_temp, uint32_t u, int exclude);
+/* the same over bf16 logits with top-p only */
 void or_dist_build(const uint16_t* logits, int V, float temperature, float top_p, or_dist* d);
 uint64_t or_dist_mass(const or_dist* d, const uint16_t* logits, float inv_temp, int token);
-/* sample with 32-bit uniform u from the kept distribution, excluding `exclude` (-1: none) */
 int or_dist_sample(const or_dist* d, const uint16_t* logits, int V, float inv_temp, uint32_t u,
                    int exclude);
+/* log(min_p) as the sampler uses it (-inf for min_p <= 0); computed once per request */
+float or_min_p_log(float min_p);
 
-struct or_sampling;
+/* Values one position samples from: the bf16 logits in fp32 after the logits processors
+ * (Sampling.swift:638-652: logit bias added in fp32 at its valid token ids, EOS ids set to
+ * -inf while fewer than min_tokens tokens were generated) and the penalties over the
+ * generated tokens (:592-636: repetition v < 0 ? v * rp : v / rp, then presence - pp, then
+ * frequency - count * fp, at each distinct generated token).  gen holds the n_gen generated
+ * tokens so far (the request's, then the drafts accepted before this position).  Returns 1
+ * when any processor or penalty applied, 0 when out[] is the plain logits. */
+int or_process_logits(const uint16_t* lg, int V, const struct or_sampling* sp, const int32_t* gen, int n_gen,
+                      float* out);
+
 /* Acceptance of one row's verify block: lg holds P+1 logits rows (position j scores
- * the token after verify token j), dr the P drafts.  Greedy rows (temperature 0) use
+ * the token after verify token j), dr the P drafts, gen the n_gen tokens the request has
+ * generated so far (penalties, min_tokens).  Greedy rows (temperature 0) use
  * `acceptance` (OR_ACCEPT_ALL_OR_NOTHING restates BatchGenerator.swift:906-947, where a
  * rejection falls back to a one-token decode whose logits are position 0); rows with
- * temperature > 0 use speculative sampling with the uniforms of (seed, counter).
- * forced_cap >= 0 caps the accepted drafts (forced accept-length schedule), -1 = none.
- * Writes the emitted tokens to out and returns their count; *kv_keep = verified
- * positions kept in the KV, *n_acc = drafts accepted (the SpeculativeDecodingStats
- * increment, :952), *rejected = 1 when a proposal was (partly) rejected (:938). */
+ * temperature > 0 use speculative sampling with the uniforms of (seed, counter), or the
+ * caller's: uniforms[j][0] the accept test and uniforms[j][1] the sample draw of position
+ * j (NULL = derived).  forced_cap >= 0 caps the accepted drafts (forced accept-length
+ * schedule), -1 = none.  Writes the emitted tokens to out and returns their count;
+ * *kv_keep = verified positions kept in the KV, *n_acc = drafts accepted (the
+ * SpeculativeDecodingStats increment, :952), *rejected = 1 when a proposal was (partly)
+ * rejected (:938). */
 int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const struct or_sampling* sp,
-                  uint64_t seed, uint64_t counter, int acceptance, int forced_cap, int32_t* out,
-                  int* kv_keep, int* n_acc, int* rejected);
+                  const int32_t* gen, int n_gen, uint64_t seed, uint64_t counter, const uint32_t* uniforms,
+                  int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc, int* rejected);
 
 /* ---- KV trim known answer: BatchCache.swift:403-424 ---- */
 /* Uniform trim of a left-padded batch: returns trimmed count, updates idx,
@@ -180,6 +208,14 @@ typedef struct or_sampling {      /* subset of SamplingParameters, Sampling.swif
   int n_eos;
   int32_t eos[8];
   int32_t reject_token;          /* QwenXMLToolGrammar toolCallStartTokenID; -1 = none */
+  int32_t top_k;                 /* 0 = off */
+  float min_p;                   /* 0 = off */
+  float repetition_penalty;      /* 1 = off (0 is read as 1) */
+  float presence_penalty, frequency_penalty;
+  int32_t min_tokens;
+  int32_t n_bias;                /* logit bias entries, at most 16 */
+  int32_t bias_token[16];
+  float bias_value[16];
 } or_sampling;
 
 typedef struct or_stats {         /* SpeculativeDecodingStats, BatchGenerator.swift:31-38 */

@@ -167,77 +167,175 @@ static inline float canon(uint16_t h) {  /* -0 -> +0 */
   return v == 0.0f ? 0.0f : v;
 }
 
-typedef struct { float v; uint64_t w; } vw_t;
-static int cmp_desc(const void* a, const void* b) {
-  float x = ((const vw_t*)a)->v, y = ((const vw_t*)b)->v;
-  return x < y ? 1 : (x > y ? -1 : 0);
+static int is_eos_tok(const or_sampling* sp, int tok) {
+  for (int i = 0; i < sp->n_eos; ++i)
+    if (sp->eos[i] == tok) return 1;
+  return 0;
 }
 
-void or_dist_build(const uint16_t* logits, int V, float temperature, float top_p, or_dist* d) {
+static int penalties_on(const or_sampling* sp) {
+  const float rp = sp->repetition_penalty == 0.0f ? 1.0f : sp->repetition_penalty;
+  return rp != 1.0f || sp->presence_penalty != 0.0f || sp->frequency_penalty != 0.0f;
+}
+
+int or_process_logits(const uint16_t* lg, int V, const or_sampling* sp, const int32_t* gen, int n_gen,
+                      float* out) {
+  for (int i = 0; i < V; ++i) out[i] = canon(lg[i]);
+  int applied = 0;
+  /* applyLogitBias, Sampling.swift:695-704: ids outside [0, V) are ignored */
+  for (int k = 0; k < sp->n_bias; ++k) {
+    const int t = sp->bias_token[k];
+    if (t >= 0 && t < V) { out[t] = out[t] + sp->bias_value[k]; applied = 1; }
+  }
+  /* shouldApplyMinTokens + maskTokens, :677-684 and :648-650 */
+  if (sp->min_tokens > 0 && n_gen < sp->min_tokens && sp->n_eos > 0) {
+    for (int k = 0; k < sp->n_eos; ++k)
+      if (sp->eos[k] >= 0 && sp->eos[k] < V) out[sp->eos[k]] = -INFINITY;
+    applied = 1;
+  }
+  /* applyPenalties, :592-636 (nothing to do without generated tokens, :597) */
+  if (penalties_on(sp) && n_gen > 0) {
+    const float rp = sp->repetition_penalty == 0.0f ? 1.0f : sp->repetition_penalty;
+    int32_t* cnt = (int32_t*)calloc((size_t)V, sizeof(int32_t));
+    for (int i = 0; i < n_gen; ++i)
+      if (gen[i] >= 0 && gen[i] < V) cnt[gen[i]]++;
+    for (int t = 0; t < V; ++t) {
+      if (!cnt[t]) continue;
+      float v = out[t];
+      if (rp != 1.0f) v = v < 0.0f ? v * rp : v / rp;
+      if (sp->presence_penalty != 0.0f) v = v - sp->presence_penalty;
+      if (sp->frequency_penalty != 0.0f) v = v - (float)cnt[t] * sp->frequency_penalty;
+      out[t] = v;
+    }
+    free(cnt);
+    applied = 1;
+  }
+  for (int i = 0; i < V; ++i)
+    if (out[i] == 0.0f) out[i] = 0.0f; /* -0 -> +0 */
+  return applied;
+}
+
+float or_min_p_log(float min_p) { return min_p > 0.0f ? logf(min_p) : -INFINITY; }
+
+static int argmax_f(const float* v, int V) {
+  int best = 0;
+  for (int i = 1; i < V; ++i)
+    if (v[i] > v[best]) best = i;
+  return best;
+}
+
+typedef struct { float v; uint64_t w; int i; } vw_t;
+static int cmp_desc(const void* a, const void* b) {  /* value descending, index ascending */
+  const vw_t* x = (const vw_t*)a;
+  const vw_t* y = (const vw_t*)b;
+  if (x->v != y->v) return x->v < y->v ? 1 : -1;
+  return x->i < y->i ? -1 : (x->i > y->i ? 1 : 0);
+}
+
+static inline int kept(const or_dist* d, float v, int i) {
+  if (d->filtered && v < d->tau) return 0;
+  if (!(v - d->max_logit >= d->min_p_log)) return 0;
+  if (v < d->topk_value || (v == d->topk_value && i > d->topk_index)) return 0;
+  return 1;
+}
+
+void or_dist_build_f(const float* v, int V, float temperature, float top_p, int top_k, float min_p_log,
+                     or_dist* d) {
   float m = -INFINITY;
-  for (int i = 0; i < V; ++i) { float v = canon(logits[i]); if (v > m) m = v; }
+  for (int i = 0; i < V; ++i) if (v[i] > m) m = v[i];
   d->max_logit = m;
   d->filtered = (top_p > 0.0f && top_p < 1.0f);
   d->tau = -INFINITY;
-  if (d->filtered) {
-    /* Sampling.swift:847-858: drop sorted positions whose mass strictly above is
-     * >= topP * total; keep every token whose logit is >= the first kept value. */
+  d->min_p_log = min_p_log;
+  d->topk_value = -INFINITY;
+  d->topk_index = 0x7FFFFFFF;
+  const int use_k = top_k > 0 && top_k < V;
+  if (d->filtered || use_k) {
     vw_t* a = (vw_t*)malloc(sizeof(vw_t) * (size_t)V);
     uint64_t total1 = 0;
     for (int i = 0; i < V; ++i) {
-      a[i].v = canon(logits[i]);
-      a[i].w = mass_of(or_exp_neg(a[i].v - m));
+      a[i].v = v[i];
+      a[i].i = i;
+      a[i].w = mass_of(or_exp_neg(v[i] - m));
       total1 += a[i].w;
     }
     qsort(a, (size_t)V, sizeof(vw_t), cmp_desc);
-    double X = (double)top_p * (double)total1;
-    uint64_t above = 0;
-    int i = 0;
-    while (i < V) {
-      float v = a[i].v;
-      if (!((double)above < X)) break;
-      d->tau = v;
-      while (i < V && a[i].v == v) { above += a[i].w; ++i; }
+    if (d->filtered) {
+      /* Sampling.swift:847-858: drop sorted positions whose mass strictly above is
+       * >= topP * total; keep every token whose value is >= the first kept value. */
+      double X = (double)top_p * (double)total1;
+      uint64_t above = 0;
+      int i = 0;
+      while (i < V) {
+        float x = a[i].v;
+        if (!((double)above < X)) break;
+        d->tau = x;
+        while (i < V && a[i].v == x) { above += a[i].w; ++i; }
+      }
+    }
+    if (use_k) {  /* Sampling.swift:893-906 */
+      d->topk_value = a[top_k - 1].v;
+      d->topk_index = a[top_k - 1].i;
     }
     free(a);
   }
   float inv_t = 1.0f / temperature;
   uint64_t tot = 0;
-  for (int i = 0; i < V; ++i) {
-    float v = canon(logits[i]);
-    if (d->filtered && v < d->tau) continue;
-    tot += mass_of(or_exp_neg((v - m) * inv_t));
-  }
+  for (int i = 0; i < V; ++i)
+    if (kept(d, v[i], i)) tot += mass_of(or_exp_neg((v[i] - m) * inv_t));
   d->total = tot;
 }
 
-uint64_t or_dist_mass(const or_dist* d, const uint16_t* logits, float inv_temp, int token) {
-  float v = canon(logits[token]);
-  if (d->filtered && v < d->tau) return 0;
-  return mass_of(or_exp_neg((v - d->max_logit) * inv_temp));
+uint64_t or_dist_mass_f(const or_dist* d, const float* v, float inv_temp, int token) {
+  if (!kept(d, v[token], token)) return 0;
+  return mass_of(or_exp_neg((v[token] - d->max_logit) * inv_temp));
 }
 
-int or_dist_sample(const or_dist* d, const uint16_t* logits, int V, float inv_temp, uint32_t u,
-                   int exclude) {
+int or_dist_sample_f(const or_dist* d, const float* v, int V, float inv_temp, uint32_t u, int exclude) {
   uint64_t total = d->total;
-  if (exclude >= 0) total -= or_dist_mass(d, logits, inv_temp, exclude);
+  if (exclude >= 0) total -= or_dist_mass_f(d, v, inv_temp, exclude);
   unsigned __int128 prod = (unsigned __int128)u * (unsigned __int128)total;
   uint64_t R = (uint64_t)(prod >> 32);
   uint64_t c = 0;
   int last = -1;
   for (int i = 0; i < V; ++i) {
     if (i == exclude) continue;
-    uint64_t w = or_dist_mass(d, logits, inv_temp, i);
+    uint64_t w = or_dist_mass_f(d, v, inv_temp, i);
     if (w == 0) continue;
     last = i;
     if (c + w > R) return i;
     c += w;
   }
-  return last; /* unreachable when total > 0 */
+  return last < 0 ? 0 : last; /* last < 0 only when nothing has mass */
 }
 
-static int accept_draft(const or_dist* d, const uint16_t* logits, float inv_temp, int x, uint32_t u) {
-  uint64_t w = or_dist_mass(d, logits, inv_temp, x);
+static float* canon_row(const uint16_t* logits, int V) {
+  float* v = (float*)malloc(sizeof(float) * (size_t)V);
+  for (int i = 0; i < V; ++i) v[i] = canon(logits[i]);
+  return v;
+}
+
+void or_dist_build(const uint16_t* logits, int V, float temperature, float top_p, or_dist* d) {
+  float* v = canon_row(logits, V);
+  or_dist_build_f(v, V, temperature, top_p, 0, -INFINITY, d);
+  free(v);
+}
+
+uint64_t or_dist_mass(const or_dist* d, const uint16_t* logits, float inv_temp, int token) {
+  const float x = canon(logits[token]);
+  if (!kept(d, x, token)) return 0;
+  return mass_of(or_exp_neg((x - d->max_logit) * inv_temp));
+}
+
+int or_dist_sample(const or_dist* d, const uint16_t* logits, int V, float inv_temp, uint32_t u, int exclude) {
+  float* v = canon_row(logits, V);
+  const int t = or_dist_sample_f(d, v, V, inv_temp, u, exclude);
+  free(v);
+  return t;
+}
+
+static int accept_draft(const or_dist* d, const float* v, float inv_temp, int x, uint32_t u) {
+  uint64_t w = or_dist_mass_f(d, v, inv_temp, x);
   unsigned __int128 lhs = (unsigned __int128)u * (unsigned __int128)d->total;
   unsigned __int128 rhs = (unsigned __int128)w << 32;
   return lhs < rhs;
@@ -246,30 +344,43 @@ static int accept_draft(const or_dist* d, const uint16_t* logits, float inv_temp
 /* ------------------------------------------------------------------ */
 /* acceptance of one row's verify block                                 */
 /* ------------------------------------------------------------------ */
-static int is_eos_tok(const or_sampling* sp, int tok) {
-  for (int i = 0; i < sp->n_eos; ++i)
-    if (sp->eos[i] == tok) return 1;
-  return 0;
+/* the values position j samples from: generated tokens so far = gen + dr[0 .. j) */
+static void position_values(const uint16_t* lg, int V, const or_sampling* sp, const int32_t* gen, int n_gen,
+                            const int32_t* dr, int j, int32_t* scratch, float* out) {
+  if (n_gen > 0) memcpy(scratch, gen, sizeof(int32_t) * (size_t)n_gen);
+  if (j > 0) memcpy(scratch + n_gen, dr, sizeof(int32_t) * (size_t)j);
+  or_process_logits(lg, V, sp, scratch, n_gen + j, out);
 }
 
-int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_sampling* sp, uint64_t seed,
-                  uint64_t counter, int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc,
-                  int* rejected) {
+static uint32_t draw(const uint32_t* uniforms, uint64_t seed, uint64_t counter, int pos, int kind) {
+  return uniforms ? uniforms[2 * pos + kind] : or_uniform_u32(seed, counter, (uint32_t)pos, (uint32_t)kind);
+}
+
+int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_sampling* sp,
+                  const int32_t* gen, int n_gen, uint64_t seed, uint64_t counter, const uint32_t* uniforms,
+                  int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc, int* rejected) {
   const int sampled = sp->temperature != 0.0f;
   const float inv_t = sampled ? 1.0f / sp->temperature : 0.0f;
+  const float lmp = or_min_p_log(sp->min_p);
+  float* v = (float*)malloc(sizeof(float) * (size_t)V);
+  int32_t* gbuf = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n_gen + P + 1));
   int n_emit = 0;
   *kv_keep = 1;
   *n_acc = 0;
   *rejected = 0;
+#define VALUES(pos) position_values(lg + (size_t)(pos) * V, V, sp, gen, n_gen, dr, (pos), gbuf, v)
   if (!sampled && acceptance == OR_ACCEPT_ALL_OR_NOTHING) {
     /* BatchGenerator.swift:906-947 */
     if (P == 0) {                                                  /* plain decodeOneToken */
-      out[0] = or_argmax_bf16(lg, V);
+      VALUES(0);
+      out[0] = argmax_f(v, V);
+      free(v); free(gbuf);
       return 1;
     }
     int all = 1, na = 0;
     for (int pos = 0; pos <= P; ++pos) {
-      const int s = or_argmax_bf16(lg + (size_t)pos * V, V);
+      VALUES(pos);   /* generatedHistory grows by the accepted tokens, :930; they equal the drafts */
+      const int s = argmax_f(v, V);
       if (sp->reject_token >= 0 && s == sp->reject_token) { all = 0; break; }  /* :920-923 */
       if (pos < P && s != dr[pos]) { all = 0; break; }                         /* :925-928 */
       out[na++] = s;
@@ -278,11 +389,14 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
     if (!all) {
       *rejected = 1;                                               /* :938 */
       /* :939 decodeOneToken on the original cache: the same logits as position 0 */
-      out[0] = or_argmax_bf16(lg, V);
+      VALUES(0);
+      out[0] = argmax_f(v, V);
+      free(v); free(gbuf);
       return 1;
     }
     *kv_keep = P + 1;                                              /* :942 adopt the working cache */
     *n_acc = na > 1 ? na - 1 : 0;                                  /* :952 */
+    free(v); free(gbuf);
     return na;
   }
   /* prefix acceptance (greedy) and speculative sampling (temperature > 0): accept drafts
@@ -293,10 +407,10 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
   if (forced_cap >= 0 && forced_cap < cap) cap = forced_cap;
   int a = 0, stop = 0;
   for (int pos = 0; pos < P; ++pos) {
-    const uint16_t* row_lg = lg + (size_t)pos * V;
+    VALUES(pos);
     int tok;
     if (!sampled) {
-      tok = or_argmax_bf16(row_lg, V);
+      tok = argmax_f(v, V);
       if (pos >= cap || tok != dr[pos] || tok == sp->reject_token) {
         out[n_emit++] = tok;
         stop = 1;
@@ -304,11 +418,10 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
       }
     } else {
       or_dist d;
-      or_dist_build(row_lg, V, sp->temperature, sp->top_p, &d);
-      const int ok = pos < cap && accept_draft(&d, row_lg, inv_t, dr[pos],
-                                               or_uniform_u32(seed, counter, (uint32_t)pos, 0));
+      or_dist_build_f(v, V, sp->temperature, sp->top_p, sp->top_k, lmp, &d);
+      const int ok = pos < cap && accept_draft(&d, v, inv_t, dr[pos], draw(uniforms, seed, counter, pos, 0));
       if (!ok) {
-        out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t, or_uniform_u32(seed, counter, (uint32_t)pos, 1), dr[pos]);
+        out[n_emit++] = or_dist_sample_f(&d, v, V, inv_t, draw(uniforms, seed, counter, pos, 1), dr[pos]);
         stop = 1;
         break;
       }
@@ -319,18 +432,21 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
     if (tok == sp->reject_token || is_eos_tok(sp, tok)) { stop = 1; break; }
   }
   if (!stop) {
-    const uint16_t* row_lg = lg + (size_t)P * V;
+    VALUES(P);
     if (sampled) {
       or_dist d;
-      or_dist_build(row_lg, V, sp->temperature, sp->top_p, &d);
-      out[n_emit++] = or_dist_sample(&d, row_lg, V, inv_t, or_uniform_u32(seed, counter, (uint32_t)P, 1), -1);
+      or_dist_build_f(v, V, sp->temperature, sp->top_p, sp->top_k, lmp, &d);
+      out[n_emit++] = or_dist_sample_f(&d, v, V, inv_t, draw(uniforms, seed, counter, P, 1), -1);
     } else {
-      out[n_emit++] = or_argmax_bf16(row_lg, V);
+      out[n_emit++] = argmax_f(v, V);
     }
   }
+#undef VALUES
   *kv_keep = a + 1;
   *n_acc = a;
   *rejected = (P > 0 && a < P) ? 1 : 0;
+  free(v);
+  free(gbuf);
   return n_emit;
 }
 
@@ -422,12 +538,11 @@ static int is_eos(const or_sampling* sp, int tok) {
   return 0;
 }
 
-/* sample one position: greedy argmax at T == 0, else integer-mass sampling */
-static int sample_pos(const or_row* rw, const uint16_t* lg, int V, uint32_t u) {
-  if (rw->sp.temperature == 0.0f) return or_argmax_bf16(lg, V);
-  or_dist d;
-  or_dist_build(lg, V, rw->sp.temperature, rw->sp.top_p, &d);
-  return or_dist_sample(&d, lg, V, 1.0f / rw->sp.temperature, u, -1);
+/* the generated tokens of a row (generatedTokenHistory): the last `generated` entries of
+ * its history */
+static const int32_t* generated_of(const or_row* rw, int* n) {
+  *n = rw->generated < rw->hist_len ? rw->generated : rw->hist_len;
+  return rw->hist + (rw->hist_len - *n);
 }
 
 static int finish_of(const or_row* rw, int tok) {   /* Scheduler.swift:1215-1227 */
@@ -454,7 +569,9 @@ int or_generator_insert(or_generator* g, int row, const int32_t* prompt, int n_p
   rw->sp = *sp;
   rw->seed = sp->has_seed ? sp->seed : or_mix64(g->global_seed ^ or_mix64(++g->unseeded_count));
   rw->counter = 0;
-  int tok = sample_pos(rw, lg, V, or_uniform_u32(rw->seed, rw->counter, 0, 1));
+  int tok, keep, nacc, rej;
+  or_accept_row(lg, V, NULL, 0, sp, NULL, 0, rw->seed, rw->counter, NULL, g->cfg.acceptance, -1, &tok, &keep, &nacc,
+                &rej);
   rw->counter++;
   free(lg);
   rw->generated = 1;
@@ -546,10 +663,11 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
     const int r = rows[i], P = nprop[r];
     or_row* rw = &g->rows[r];
     int32_t* out = out_tokens + (size_t)r * (K + 1);
-    int kv_keep = 1, n_acc = 0, rejected = 0;
-    const int n_emit = or_accept_row(lg + (size_t)t0 * V, V, drafts + (size_t)r * (K + 1), P, &rw->sp, rw->seed,
-                                     rw->counter, g->cfg.acceptance, forced_accept ? forced_accept[r] : -1, out,
-                                     &kv_keep, &n_acc, &rejected);
+    int kv_keep = 1, n_acc = 0, rejected = 0, n_gen = 0;
+    const int32_t* gen = generated_of(rw, &n_gen);
+    const int n_emit = or_accept_row(lg + (size_t)t0 * V, V, drafts + (size_t)r * (K + 1), P, &rw->sp, gen, n_gen,
+                                     rw->seed, rw->counter, NULL, g->cfg.acceptance,
+                                     forced_accept ? forced_accept[r] : -1, out, &kv_keep, &n_acc, &rejected);
     if (P > 0) {
       g->stats.accepted += n_acc;                                     /* :952 */
       g->stats.rejected_batches += rejected;                          /* :938 */

@@ -46,7 +46,10 @@ class SpecConfig(C.Structure):
 class Sampling(C.Structure):
     _fields_ = [
         ("temperature", C.c_float), ("top_p", C.c_float), ("has_seed", C.c_int), ("seed", C.c_uint64),
-        ("n_eos", C.c_int), ("eos", C.c_int32 * 8), ("reject_token", C.c_int32),
+        ("n_eos", C.c_int), ("eos", C.c_int32 * 8), ("reject_token", C.c_int32), ("top_k", C.c_int32),
+        ("min_p", C.c_float), ("repetition_penalty", C.c_float), ("presence_penalty", C.c_float),
+        ("frequency_penalty", C.c_float), ("min_tokens", C.c_int32), ("n_bias", C.c_int32),
+        ("bias_token", C.c_int32 * 16), ("bias_value", C.c_float * 16),
     ]
 
 
@@ -56,7 +59,8 @@ class Stats(C.Structure):
 
 
 class Dist(C.Structure):
-    _fields_ = [("total", C.c_uint64), ("max_logit", C.c_float), ("tau", C.c_float), ("filtered", C.c_int)]
+    _fields_ = [("total", C.c_uint64), ("max_logit", C.c_float), ("tau", C.c_float), ("filtered", C.c_int),
+                ("min_p_log", C.c_float), ("topk_value", C.c_float), ("topk_index", C.c_int32)]
 
 
 _lib = None
@@ -83,8 +87,13 @@ def lib():
             "or_dist_build": (None, [P, I, F, F, P]),
             "or_dist_mass": (U64, [P, P, F, I]),
             "or_dist_sample": (I, [P, P, I, F, U32, I]),
+            "or_dist_build_f": (None, [P, I, F, F, I, F, P]),
+            "or_dist_mass_f": (U64, [P, P, F, I]),
+            "or_dist_sample_f": (I, [P, P, I, F, U32, I]),
+            "or_min_p_log": (F, [F]),
+            "or_process_logits": (I, [P, I, P, P, I, P]),
             "or_batch_trim": (I, [P, I, P, P, I]),
-            "or_accept_row": (I, [P, I, P, I, P, U64, U64, I, I, P, P, P, P]),
+            "or_accept_row": (I, [P, I, P, I, P, P, I, U64, U64, P, I, I, P, P, P, P]),
             "or_qmatmul": (None, [P, P, P, I, I, P, I, P]),
             "or_model_create": (P, [P, U64, I, I]),
             "or_model_destroy": (None, [P]),
@@ -164,18 +173,34 @@ def qmatmul(wq, s, b, x) -> np.ndarray:
 
 
 def accept_row(logits_bf16: np.ndarray, drafts, sampling: "Sampling", seed: int, counter: int, acceptance: int,
-               forced_cap: int = -1):
-    """Acceptance of one row: logits_bf16 [P+1][V] uint16, drafts P tokens.
+               forced_cap: int = -1, generated=(), uniforms=None):
+    """Acceptance of one row: logits_bf16 [P+1][V] uint16, drafts P tokens, `generated` the
+    request's generated tokens so far, `uniforms` [P+1][2] caller draws (None = derived).
     Returns (emitted tokens, kv_keep, n_accepted, rejected)."""
     lg = np.ascontiguousarray(logits_bf16, dtype=np.uint16)
     dr = i32(drafts) if len(drafts) else np.zeros(1, dtype=np.int32)
     P = len(drafts)
     assert lg.shape[0] == P + 1
+    gen = i32(generated) if len(generated) else np.zeros(1, dtype=np.int32)
+    u = None
+    if uniforms is not None:
+        u = np.ascontiguousarray(uniforms, dtype=np.uint32).reshape(-1)
+        assert u.size >= 2 * (P + 1)
     out = np.zeros(P + 1, dtype=np.int32)
     keep, nacc, rej = C.c_int(), C.c_int(), C.c_int()
-    n = lib().or_accept_row(_p(lg), lg.shape[1], _p(dr), P, C.byref(sampling), seed, counter, acceptance,
-                            forced_cap, _p(out), C.byref(keep), C.byref(nacc), C.byref(rej))
+    n = lib().or_accept_row(_p(lg), lg.shape[1], _p(dr), P, C.byref(sampling), _p(gen), len(generated), seed,
+                            counter, _p(u) if u is not None else None, acceptance, forced_cap, _p(out),
+                            C.byref(keep), C.byref(nacc), C.byref(rej))
     return out[:n].tolist(), keep.value, nacc.value, rej.value
+
+
+def process_logits(logits_bf16: np.ndarray, sampling: "Sampling", generated=()) -> np.ndarray:
+    """The fp32 values one position samples from (bias, min_tokens mask, penalties)."""
+    lg = np.ascontiguousarray(logits_bf16, dtype=np.uint16)
+    gen = i32(generated) if len(generated) else np.zeros(1, dtype=np.int32)
+    out = np.zeros(len(lg), dtype=np.float32)
+    lib().or_process_logits(_p(lg), len(lg), C.byref(sampling), _p(gen), len(generated), _p(out))
+    return out
 
 
 def dist_build(logits_bf16: np.ndarray, temperature: float, top_p: float) -> Dist:
@@ -183,6 +208,20 @@ def dist_build(logits_bf16: np.ndarray, temperature: float, top_p: float) -> Dis
     d = Dist()
     lib().or_dist_build(_p(lg), len(lg), temperature, top_p, C.byref(d))
     return d
+
+
+def dist_build_f(values: np.ndarray, temperature: float, top_p: float = 0.0, top_k: int = 0,
+                 min_p: float = 0.0) -> Dist:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    d = Dist()
+    lib().or_dist_build_f(_p(v), len(v), temperature, top_p, top_k, lib().or_min_p_log(min_p), C.byref(d))
+    return d
+
+
+def kept_mask(d: Dist, values: np.ndarray) -> np.ndarray:
+    """Tokens with positive mass at temperature 1 under the filters of d."""
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    return np.array([lib().or_dist_mass_f(C.byref(d), _p(v), 1.0, i) > 0 for i in range(len(v))])
 
 
 class Model:
@@ -252,7 +291,9 @@ class reversed_reduction_order:
         return False
 
 
-def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1) -> Sampling:
+def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1, top_k=0, min_p=0.0,
+                  repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0, min_tokens=0,
+                  logit_bias=None) -> Sampling:
     sp = Sampling()
     sp.temperature = temperature
     sp.top_p = top_p
@@ -262,6 +303,18 @@ def make_sampling(temperature=0.0, top_p=0.0, seed=None, eos=(), reject_token=-1
     for i, e in enumerate(eos):
         sp.eos[i] = e
     sp.reject_token = reject_token
+    sp.top_k = top_k
+    sp.min_p = min_p
+    sp.repetition_penalty = repetition_penalty
+    sp.presence_penalty = presence_penalty
+    sp.frequency_penalty = frequency_penalty
+    sp.min_tokens = max(0, min_tokens)
+    bias = sorted((logit_bias or {}).items())
+    assert len(bias) <= 16
+    sp.n_bias = len(bias)
+    for i, (t, b) in enumerate(bias):
+        sp.bias_token[i] = t
+        sp.bias_value[i] = b
     return sp
 
 

@@ -169,6 +169,16 @@ unsigned long long shfl_xor_u64(unsigned long long v, int mask) {
   });
   return W.qo[l];
 }
+unsigned long long shfl_idx_u64(unsigned long long v, int src) {
+  Wave& W = my_wave();
+  const int l = my_lane();
+  W.q[l] = v;
+  W.src[l] = src;
+  arrive(W, K_SHFL_U64, [](Wave& w) {
+    for (int k = 0; k < 64; ++k) w.qo[k] = w.q[(w.src[k] >= 0 && w.src[k] < 64) ? w.src[k] : k];
+  });
+  return W.qo[l];
+}
 unsigned shfl_u(unsigned v, int src) {
   Wave& W = my_wave();
   const int l = my_lane();

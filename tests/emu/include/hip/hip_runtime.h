@@ -116,6 +116,7 @@ float shfl_xor_f(float v, int mask);
 int shfl_xor_i(int v, int mask);
 unsigned long long shfl_xor_u64(unsigned long long v, int mask);
 unsigned shfl_u(unsigned v, int src);
+unsigned long long shfl_idx_u64(unsigned long long v, int src);
 int any(int pred);
 unsigned long long ballot(int pred);
 void wave_sync();
@@ -163,6 +164,12 @@ inline unsigned long long __shfl_xor(unsigned long long v, int mask, int width =
   return emu::shfl_xor_u64(v, mask);
 }
 inline unsigned __shfl(unsigned v, int src) { return emu::shfl_u(v, src); }
+// lane l reads lane l - delta; lanes below delta keep their own value
+inline unsigned long long __shfl_up(unsigned long long v, unsigned delta, int width = 64) {
+  (void)width;
+  const int l = (int)(threadIdx.x & 63), s = l - (int)delta;
+  return emu::shfl_idx_u64(v, s < 0 ? l : s);
+}
 // DPP moves used by the kernels: quad_perm (ctrl < 0x100) and the half-row mirror (0x141),
 // every row and bank enabled
 inline int emu_dpp(int src, int ctrl) {

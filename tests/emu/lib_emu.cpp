@@ -10,6 +10,7 @@
 //   case 4: the case-3 model through mc_step (verify blocks with padding slots; MC_STEP_EAGER=1)
 //   case 5: a small Qwen3-MoE model (16 experts, top-4)
 //   case 6: the case-0 model, 12 rows: one verify block of 12 x 6 = 72 tokens (the M > 64 GEMM)
+//   case 7: mc_accept with random sampler options against or_accept_row
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -54,10 +55,110 @@ static void compare(const char* what, const uint16_t* got, const uint16_t* want,
   if (out > allowed) ++g_bad;
 }
 
+// case 7: mc_accept over host logits with random sampler options (temperature, top-p,
+// top-k, min-p, logit bias, min_tokens, penalties over generated histories, caller or
+// derived uniforms) against or_accept_row, token for token.
+static uint64_t rng_state = 0x1234567ull;
+static uint32_t rnd(uint32_t n) { return (uint32_t)(or_mix64(rng_state++) % n); }
+
+static int accept_case(int argc_trials) {
+  const int V = 3000, B = 6, KD = 5;
+  const int trials = argc_trials > 0 ? argc_trials : 12;
+  for (int trial = 0; trial < trials; ++trial) {
+    std::vector<int32_t> nd(B), dr((size_t)B * KD, 0);
+    std::vector<int64_t> off(B + 1, 0), goff(B + 1, 0);
+    std::vector<int32_t> gen;
+    std::vector<mc_sampling> sp(B);
+    std::vector<or_sampling> osp(B);
+    std::vector<uint64_t> ctr(B);
+    const bool use_u = trial % 2 == 1;
+    std::vector<uint32_t> uni((size_t)B * (KD + 1) * 2);
+    for (auto& u : uni) u = (uint32_t)or_mix64(rng_state++);
+    for (int r = 0; r < B; ++r) {
+      nd[r] = (int)rnd(KD + 1);
+      off[r + 1] = off[r] + nd[r] + 1;
+      ctr[r] = rnd(100);
+      mc_sampling q;
+      memset(&q, 0, sizeof q);
+      const float temps[] = {0.f, 0.7f, 1.0f, 1.5f};
+      const float tops[] = {0.f, 0.9f, 0.5f};
+      const int topks[] = {0, 1, 5, 50};
+      const float minps[] = {0.f, 0.05f, 0.3f};
+      const float reps[] = {1.f, 1.3f, 0.8f, 0.f};
+      q.temperature = temps[rnd(4)];
+      q.top_p = tops[rnd(3)];
+      q.top_k = topks[rnd(4)];
+      q.min_p = minps[rnd(3)];
+      q.repetition_penalty = reps[rnd(4)];
+      q.presence_penalty = rnd(2) ? 0.5f : 0.f;
+      q.frequency_penalty = rnd(2) ? 0.25f : 0.f;
+      q.min_tokens = 0;  // set below, around the generated count
+      q.has_seed = 1;
+      q.seed = or_mix64(trial * 100 + r);
+      q.n_eos = (int)rnd(3);
+      for (int i = 0; i < q.n_eos; ++i) q.eos[i] = (int)rnd(rnd(2) ? 12 : 40);
+      q.reject_token = -1;
+      q.n_bias = (int)rnd(4);
+      for (int i = 0; i < q.n_bias; ++i) {
+        q.bias_token[i] = rnd(8) == 0 ? V + 5 : (int)rnd(40);
+        q.bias_value[i] = rnd(2) ? 2.5f : -1.75f;
+      }
+      // generated tokens from a small pool (counts above 1), drafts often from it too
+      const int ng = (int)rnd(16);
+      for (int i = 0; i < ng; ++i) gen.push_back((int)rnd(12));
+      goff[r + 1] = goff[r] + ng;
+      if (rnd(2)) q.min_tokens = ng + (int)rnd(4);  // the mask ends inside the verify block
+      for (int j = 0; j < nd[r]; ++j) dr[(size_t)r * KD + j] = (int)rnd(rnd(2) ? 12 : 40);
+      sp[r] = q;
+      static_assert(sizeof(mc_sampling) == sizeof(or_sampling), "same layout");
+      memcpy(&osp[r], &q, sizeof q);
+    }
+    // logits: few distinct bf16 values (ties everywhere), the first 40 ids larger
+    std::vector<uint16_t> lg((size_t)off[B] * V);
+    for (size_t i = 0; i < lg.size(); ++i) {
+      const int id = (int)(i % V);
+      const float v = id < 12 ? (float)((int)rnd(12) + 6) * 0.5f
+                      : id < 40 ? (float)((int)rnd(24) - 4) * 0.5f : (float)((int)rnd(16) - 20) * 0.5f;
+      lg[i] = or_f32_to_bf16(v);
+    }
+    std::vector<int32_t> out((size_t)B * (KD + 1)), ne(B), keep(B), nacc(B);
+    check(mc_accept(lg.data(), V, B, off.data(), dr.data(), KD, nd.data(), sp.data(), gen.data(), goff.data(),
+                    ctr.data(), use_u ? uni.data() : nullptr, trial % 3 == 0 ? 0 : 1, out.data(), ne.data(), keep.data(),
+                    nacc.data()),
+          "mc_accept");
+    for (int r = 0; r < B; ++r) {
+      std::vector<int32_t> want(KD + 1);
+      int wk, wn, wr;
+      const int n = or_accept_row(lg.data() + (size_t)off[r] * V, V, dr.data() + (size_t)r * KD, nd[r], &osp[r],
+                                  gen.data() + goff[r], (int)(goff[r + 1] - goff[r]), sp[r].seed, ctr[r],
+                                  use_u ? uni.data() + (size_t)r * (KD + 1) * 2 : nullptr, trial % 3 == 0 ? 0 : 1, -1,
+                                  want.data(), &wk, &wn, &wr);
+      bool same = n == ne[r] && wk == keep[r] && wn == nacc[r];
+      for (int j = 0; same && j < n; ++j) same = want[j] == out[(size_t)r * (KD + 1) + j];
+      if (!same) {
+        ++g_bad;
+        printf("trial %d row %d: T %.2f top_p %.2f top_k %d min_p %.2f rp %.2f pp %.2f fp %.2f min_tokens %d "
+               "bias %d: got n %d keep %d acc %d [%d %d], want n %d keep %d acc %d [%d %d]\n",
+               trial, r, sp[r].temperature, sp[r].top_p, sp[r].top_k, sp[r].min_p, sp[r].repetition_penalty,
+               sp[r].presence_penalty, sp[r].frequency_penalty, sp[r].min_tokens, sp[r].n_bias, ne[r], keep[r],
+               nacc[r], out[(size_t)r * (KD + 1)], ne[r] > 1 ? out[(size_t)r * (KD + 1) + 1] : -1, n, wk, wn, want[0],
+               n > 1 ? want[1] : -1);
+      }
+    }
+    printf("trial %d done\n", trial);
+    fflush(stdout);
+  }
+  printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
+  if (emu::oob_loads || emu::oob_stores) ++g_bad;
+  printf("%s\n", g_bad ? "FAIL" : "OK");
+  return g_bad ? 1 : 0;
+}
+
 int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
   check(mc_set_device(0), "set_device");
+  if (cs == 7) return accept_case(argc > 2 ? atoi(argv[2]) : 0);
   mc_model_config c{};
   c.arch = 0; c.n_layers = 2; c.hidden = 256; c.n_q_heads = 4; c.n_kv_heads = 2; c.head_dim = 128;
   c.intermediate = 512; c.vocab = 4096; c.tied_embeddings = 1; c.rms_eps = 1e-6f; c.rope_theta = 1e6f;
@@ -97,7 +198,7 @@ int main(int argc, char** argv) {
       std::vector<int32_t> toks{first};
       for (int st = 0; st < 6; ++st) {
         int32_t ot[6], cnt[1], f[1];
-        check(mc_step(bb, nullptr, ot, cnt, f), "step");
+        check(mc_step(bb, nullptr, nullptr, ot, cnt, f), "step");
         for (int k = 0; k < cnt[0]; ++k) toks.push_back(ot[k]);
         if (cnt[0] == 0) break;
       }
