@@ -213,6 +213,22 @@ int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const int64_t* r
               const uint64_t* counter, const uint32_t* uniforms, int32_t acceptance,
               int32_t* out_tokens, int32_t* n_emit, int32_t* kv_keep, int32_t* n_accepted);
 
+/* ---- acceptance that allocates nothing.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same acceptance as mc_accept with no generated
+ * history, over caller DEVICE buffers: logits [B][K+1][vocab] bf16 (row r's position j at
+ * r*(K+1)+j), drafts [B][K], n_draft [B], uniforms [B][K+1][2] or NULL (derived from seed
+ * and counter), outputs out_tokens [B][K+1], n_emit, kv_keep, n_accepted [B].  sp and
+ * counter are host arrays of B entries.  At most 64 rows and K <= 16 (MC_E_CAPACITY
+ * beyond).  Its state is a 64 KiB device array per GPU, held until the process ends and
+ * shared by all calls on that GPU: calls that overlap on one GPU race.  Runs on the null
+ * stream of the device mc_set_device selected and returns after the results are written;
+ * MC_E_INVALID if an n_draft or draft id is out of range. ---- */
+int mc_accept_noalloc(const uint16_t* logits, int32_t vocab, int32_t B, int32_t K, const int32_t* drafts,
+                      const int32_t* n_draft, const mc_sampling* sp, const uint64_t* counter,
+                      const uint32_t* uniforms, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
+                      int32_t* kv_keep, int32_t* n_accepted);
+
 /* ---- fused step: ContinuousBatchGenerator.next() -> speculativeNext()
  * (BatchGenerator.swift:593-600, 875-955) plus Scheduler.step's finish handling
  * (Scheduler.swift:361-427), for every active row at once: propose, verify forward,

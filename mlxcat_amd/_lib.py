@@ -26,7 +26,7 @@ EXPORTS = [
     "mc_model_set_linear", "mc_model_get_linear", "mc_model_set_norm", "mc_batch_create", "mc_batch_destroy",
     "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
     "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_history",
-    "mc_forward", "mc_ngram_propose", "mc_accept", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
+    "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
     "mc_batch_set_profiling", "mc_batch_profile",
 ]
 
@@ -105,6 +105,7 @@ def load(path: str = LIB_PATH):
         "mc_forward": (C.c_int, [P, I32, P, P, P, P]),
         "mc_ngram_propose": (C.c_int, [P, P, I32, I32, I32, P, I32, P, P]),
         "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, P, P, P, I32, P, P, P, P]),
+        "mc_accept_noalloc": (C.c_int, [P, I32, I32, I32, P, P, P, P, P, I32, P, P, P, P]),
         "mc_step": (C.c_int, [P, P, P, P, P, P]),
         "mc_batch_stats": (C.c_int, [P, P]),
         "mc_batch_call_widths": (C.c_int, [P, P, I32]),
@@ -380,3 +381,18 @@ def accept(logits_rows: list[np.ndarray], drafts: list[list[int]], samplings: li
     _check(load().mc_accept(_p(lg), V, B, _p(off), _p(dr), stride, _p(nd), C.cast(sp, C.c_void_p), _p(gen), _p(goff),
                             _p(ctr), _p(u), acceptance, _p(out), _p(n_emit), _p(keep), _p(nacc)))
     return [out[r, : n_emit[r]].tolist() for r in range(B)], keep.tolist(), nacc.tolist()
+
+
+def accept_noalloc(logits_ptr: int, vocab: int, B: int, K: int, drafts_ptr: int, n_draft_ptr: int,
+                   samplings: list[Sampling], counters, uniforms_ptr: int | None, acceptance: int, out_ptr: int,
+                   n_emit_ptr: int, keep_ptr: int, nacc_ptr: int) -> None:
+    """mc_accept_noalloc over device buffers given as raw addresses (logits [B][K+1][V] bf16,
+    drafts [B][K], n_draft [B], uniforms [B][K+1][2] or None; outputs out [B][K+1], n_emit,
+    kv_keep, n_accepted [B], all int32)."""
+    sp = (Sampling * B)(*samplings)
+    ctr = np.ascontiguousarray(counters, dtype=np.uint64)
+    _check(load().mc_accept_noalloc(C.c_void_p(logits_ptr), vocab, B, K, C.c_void_p(drafts_ptr),
+                                    C.c_void_p(n_draft_ptr), C.cast(sp, C.c_void_p), _p(ctr),
+                                    C.c_void_p(uniforms_ptr) if uniforms_ptr else None, acceptance,
+                                    C.c_void_p(out_ptr), C.c_void_p(n_emit_ptr), C.c_void_p(keep_ptr),
+                                    C.c_void_p(nacc_ptr)))

@@ -32,6 +32,25 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
 static int g_device = 0;
 constexpr int PREFILL_CHUNK = 64;
 
+// State of mc_accept_noalloc: a file-scope device array, one copy per GPU, held until the
+// process ends and shared by every call on that GPU.  Host code never names it as an
+// address: hipGetSymbolAddress gives each device's copy (resolved once per device, with
+// that device current), and only that pointer reaches kernels and copies.
+constexpr size_t NOALLOC_SCRATCH_BYTES = 64 * 1024;
+constexpr int NOALLOC_MAX_ROWS = 64, NOALLOC_MAX_DRAFTS = 16, NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+static int resolve_scratch(int device) {  // `device` must be current
+  if (device < 0 || device >= NOALLOC_MAX_DEVICES) return fail(MC_E_INVALID, "device index beyond the scratch table");
+  if (g_scratch_ptr[device]) return MC_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+  g_scratch_ptr[device] = p;
+  return MC_OK;
+}
+
 template <typename T>
 static int dev_alloc(T** p, size_t n) {
   *p = nullptr;
@@ -118,7 +137,7 @@ extern "C" int mc_set_device(int device) {
   if (device < 0 || device >= n) return fail(MC_E_INVALID, "mc_set_device: no such device");
   g_device = device;
   MC_HIP(hipSetDevice(device));
-  return MC_OK;
+  return resolve_scratch(device);
 }
 
 static int norm_ones(uint16_t** p, int n) {
@@ -1524,4 +1543,91 @@ extern "C" int mc_accept(const uint16_t* logits, int32_t vocab, int32_t B, const
   if (st) (void)hipStreamDestroy(st);
   for (void* p : allocs) (void)hipFree(p);
   return rc;
+}
+
+// ---- acceptance over caller device buffers, allocating nothing ----
+extern "C" int mc_accept_noalloc(const uint16_t* logits, int32_t vocab, int32_t B, int32_t K, const int32_t* drafts,
+                                 const int32_t* n_draft, const mc_sampling* sp, const uint64_t* counter,
+                                 const uint32_t* uniforms, int32_t acceptance, int32_t* out_tokens, int32_t* n_emit,
+                                 int32_t* kv_keep, int32_t* n_accepted) {
+  if (!logits || !n_draft || !sp || !counter || !out_tokens || !n_emit || !kv_keep || !n_accepted || B <= 0 ||
+      vocab <= 0 || K < 0 || (K > 0 && !drafts))
+    return fail(MC_E_INVALID, "mc_accept_noalloc: bad argument");
+  if (B > NOALLOC_MAX_ROWS || K > NOALLOC_MAX_DRAFTS)
+    return fail(MC_E_CAPACITY, "mc_accept_noalloc: at most 64 rows and 16 drafts per row");
+  int rc;
+  RowSampling q[NOALLOC_MAX_ROWS];
+  for (int r = 0; r < B; ++r)
+    if ((rc = row_sampling(&sp[r], vocab, &q[r]))) return rc;
+  MC_HIP(hipSetDevice(g_device));
+  if ((rc = resolve_scratch(g_device))) return rc;
+  const int K1 = K + 1;
+  const size_t R = (size_t)B, RK = R * K1;
+  // layout in 32-bit words: the part the prep kernel fills, then the part copied from the host
+  size_t words = 0;
+  auto take = [&](size_t n) { size_t o = words; words += (n + 1) & ~(size_t)1; return o; };
+  const size_t o_np = take(R), o_nv = take(R), o_rs0 = take(R), o_act = take(R), o_dr = take(RK), o_forced = take(R),
+               o_gen = take(R), o_sct = take(RK), o_sca = take(RK), o_scr = take(RK);
+  const size_t host0 = words;
+  const size_t o_temp = take(R), o_topp = take(R), o_invt = take(R), o_hseed = take(R), o_seed = take(2 * R),
+               o_ctr = take(2 * R), o_eos = take(8 * R), o_neos = take(R), o_rej = take(R), o_topk = take(R),
+               o_mpl = take(R), o_rp = take(R), o_pp = take(R), o_fp = take(R), o_mint = take(R), o_nb = take(R),
+               o_bt = take(16 * R), o_bv = take(16 * R), o_proc = take(R), o_useu = take(2), o_err = take(2);
+  if (words * 4 > NOALLOC_SCRATCH_BYTES) return fail(MC_E_CAPACITY, "mc_accept_noalloc: scratch too small");
+  // the host part, staged in a per-thread buffer
+  static thread_local uint32_t himg[NOALLOC_SCRATCH_BYTES / 4];
+  uint32_t* h = himg - host0;  // h[o] for o >= host0
+  memset(himg, 0, (words - host0) * 4);
+  auto put_f = [&](size_t o, float v) { memcpy(&h[o], &v, 4); };
+  auto put_i = [&](size_t o, int32_t v) { memcpy(&h[o], &v, 4); };
+  for (int r = 0; r < B; ++r) {
+    put_f(o_temp + r, q[r].temp);
+    put_f(o_topp + r, q[r].top_p);
+    put_f(o_invt + r, q[r].inv_t);
+    put_i(o_hseed + r, sp[r].has_seed);
+    memcpy(&h[o_seed + 2 * r], &sp[r].seed, 8);
+    memcpy(&h[o_ctr + 2 * r], &counter[r], 8);
+    for (int i = 0; i < 8; ++i) put_i(o_eos + 8 * r + i, q[r].eos[i]);
+    put_i(o_neos + r, q[r].n_eos);
+    put_i(o_rej + r, sp[r].reject_token);
+    put_i(o_topk + r, q[r].top_k);
+    put_f(o_mpl + r, q[r].min_p_log);
+    put_f(o_rp + r, q[r].rp);
+    put_f(o_pp + r, q[r].pp);
+    put_f(o_fp + r, q[r].fp);
+    put_i(o_mint + r, q[r].min_tokens);
+    put_i(o_nb + r, q[r].n_bias);
+    for (int i = 0; i < 16; ++i) {
+      put_i(o_bt + 16 * r + i, q[r].bias_tok[i]);
+      put_f(o_bv + 16 * r + i, q[r].bias_val[i]);
+    }
+    put_i(o_proc + r, q[r].proc);
+  }
+  put_i(o_useu, uniforms ? 1 : 0);
+  uint32_t* base = static_cast<uint32_t*>(g_scratch_ptr[g_device]);
+  auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(base + o); };
+  auto F32 = [&](size_t o) { return reinterpret_cast<float*>(base + o); };
+  StepState s;
+  s.R = B; s.K = K; s.K1 = K1; s.V = vocab; s.acceptance = acceptance; s.hcap = 1;
+  s.nprop = I32(o_np); s.n_valid = I32(o_nv); s.row_slot0 = I32(o_rs0); s.active = I32(o_act); s.drafts = I32(o_dr);
+  s.forced = I32(o_forced); s.gen = I32(o_gen); s.scan_tok = I32(o_sct); s.scan_acc = I32(o_sca);
+  s.scan_res = I32(o_scr); s.temp = F32(o_temp); s.top_p = F32(o_topp); s.inv_temp = F32(o_invt);
+  s.has_seed = I32(o_hseed); s.seed = reinterpret_cast<uint64_t*>(base + o_seed);
+  s.counter = reinterpret_cast<uint64_t*>(base + o_ctr); s.eos = I32(o_eos); s.n_eos = I32(o_neos);
+  s.reject = I32(o_rej); s.top_k = I32(o_topk); s.min_p_log = F32(o_mpl); s.rep_pen = F32(o_rp);
+  s.pres_pen = F32(o_pp); s.freq_pen = F32(o_fp); s.min_tokens = I32(o_mint); s.n_bias = I32(o_nb);
+  s.bias_tok = I32(o_bt); s.bias_val = F32(o_bv); s.proc = I32(o_proc); s.use_uniforms = I32(o_useu);
+  s.uniforms = uniforms;  // caller's [B][K + 1][2]
+  s.gen_cnt = nullptr;    // no generated history: penalties see the drafts only
+  s.out_tok = out_tokens; // caller's [B][K + 1]
+  hipStream_t st = nullptr;
+  MC_HIP(hipMemcpyAsync(base + host0, himg, (words - host0) * 4, hipMemcpyHostToDevice, st));
+  if ((rc = launch_accept_prep(s, drafts, n_draft, K, I32(o_err), st))) return rc;
+  if ((rc = launch_accept_scan(s, logits, -1, st))) return rc;
+  if ((rc = launch_decide(s, n_emit, kv_keep, n_accepted, st))) return rc;
+  int32_t err = 0;
+  MC_HIP(hipMemcpyAsync(&err, I32(o_err), 4, hipMemcpyDeviceToHost, st));
+  MC_HIP(hipStreamSynchronize(st));
+  if (err) return fail(MC_E_INVALID, "mc_accept_noalloc: n_draft or a draft id out of range");
+  return MC_OK;
 }

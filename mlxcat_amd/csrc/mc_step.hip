@@ -221,7 +221,7 @@ struct PosVals {
   const int32_t* eos = nullptr;
   int pen = 0;
   float rp = 1.f, pp = 0.f, fp = 0.f;
-  const int32_t* cnt = nullptr;  // [V] generated-token counts of the row
+  const int32_t* cnt = nullptr;  // [V] generated-token counts of the row (NULL: none generated)
   const int32_t* dr = nullptr;   // drafts before this position
   int nd = 0;
   __device__ float operator()(int i) const {
@@ -233,7 +233,7 @@ struct PosVals {
       for (int k = 0; k < ne; ++k)
         if (eos[k] == i) v = -INFINITY;
       if (pen) {
-        int c = cnt[i];
+        int c = cnt ? cnt[i] : 0;
         for (int t = 0; t < nd; ++t) c += dr[t] == i;
         if (c > 0) {
           if (rp != 1.0f) v = v < 0.0f ? v * rp : v / rp;
@@ -487,7 +487,7 @@ __global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, 
     pv.rp = s.rep_pen[r];
     pv.pp = s.pres_pen[r];
     pv.fp = s.freq_pen[r];
-    pv.cnt = s.gen_cnt + (size_t)r * V;
+    pv.cnt = s.gen_cnt ? s.gen_cnt + (size_t)r * V : nullptr;
   }
   if (s.temp[r] == 0.0f) {
     int t;
@@ -661,6 +661,39 @@ __global__ void decide_kernel(StepState s, int32_t* n_emit, int32_t* keep_out, i
 
 int launch_decide(const StepState& s, int32_t* n_emit, int32_t* keep_out, int32_t* nacc_out, hipStream_t st) {
   hipLaunchKernelGGL(decide_kernel, dim3((s.R + 63) / 64), dim3(64), 0, st, s, n_emit, keep_out, nacc_out);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
+}
+
+// Rows of an acceptance over caller device buffers: drafts [B][K] -> the state's [B][K1]
+// layout, proposal lengths, slot offsets.  A row whose n_draft or draft ids are out of range
+// is run with no drafts and flagged in *err.
+__global__ void accept_prep_kernel(StepState s, const int32_t* drafts, const int32_t* n_draft, int K, int32_t* err) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= s.R) return;
+  int P = n_draft[r];
+  bool bad = P < 0 || P > K;
+  if (!bad)
+    for (int j = 0; j < P; ++j) {
+      const int t = drafts[(size_t)r * K + j];
+      bad = bad || t < 0 || t >= s.V;
+    }
+  if (bad) {
+    P = 0;
+    atomicAdd(err, 1);
+  }
+  for (int j = 0; j < s.K1; ++j) s.drafts[r * s.K1 + j] = j < P ? drafts[(size_t)r * K + j] : 0;
+  s.nprop[r] = P;
+  s.n_valid[r] = P + 1;
+  s.row_slot0[r] = r * s.K1;
+  s.active[r] = 1;
+  s.forced[r] = -1;
+  s.gen[r] = 0;
+}
+
+int launch_accept_prep(const StepState& s, const int32_t* drafts, const int32_t* n_draft, int K, int32_t* err,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(accept_prep_kernel, dim3((s.R + 63) / 64), dim3(64), 0, st, s, drafts, n_draft, K, err);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }

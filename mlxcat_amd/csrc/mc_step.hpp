@@ -73,6 +73,9 @@ int launch_propose(const StepState& s, hipStream_t st);
 int launch_accept_scan(const StepState& s, const uint16_t* logits, int row_filter, hipStream_t st);
 int launch_commit(const StepState& s, int row_filter, hipStream_t st);
 int launch_decide(const StepState& s, int32_t* n_emit, int32_t* keep_out, int32_t* nacc_out, hipStream_t st);
+// drafts [R][K] and n_draft [R] of caller device buffers into s (bad rows counted in *err)
+int launch_accept_prep(const StepState& s, const int32_t* drafts, const int32_t* n_draft, int K, int32_t* err,
+                       hipStream_t st);
 
 // standalone entry points over caller data (mc_ngram_propose / mc_accept)
 int launch_ngram_standalone(const int32_t* hist, const int64_t* off, int B, int max_suffix, int min_ctx,

@@ -74,6 +74,12 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int d);
 hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned f);
 hipError_t hipStreamDestroy(hipStream_t s);
 hipError_t hipStreamSynchronize(hipStream_t s);
+// a __device__ array is host memory here: its address is the symbol's
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+  *p = const_cast<void*>(sym);
+  return hipSuccess;
+}
 hipError_t hipGetLastError();
 const char* hipGetErrorString(hipError_t e);
 hipError_t hipFuncSetAttribute(const void* f, hipFuncAttribute a, int v);
@@ -198,6 +204,7 @@ inline float __uint_as_float(unsigned u) {
   return f;
 }
 inline unsigned atomicAdd(unsigned* p, unsigned v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
+inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
 inline unsigned long long atomicAdd(unsigned long long* p, unsigned long long v) {
   return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST);
 }

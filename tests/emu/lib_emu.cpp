@@ -11,6 +11,7 @@
 //   case 5: a small Qwen3-MoE model (16 experts, top-4)
 //   case 6: the case-0 model, 12 rows: one verify block of 12 x 6 = 72 tokens (the M > 64 GEMM)
 //   case 7: mc_accept with random sampler options against or_accept_row
+//   case 8: mc_accept_noalloc against mc_accept, two calls
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -21,6 +22,7 @@
 
 #include "../../include/mlxcat_hip.h"
 #include "emu.hpp"
+#include <hip/hip_runtime.h>
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -154,11 +156,101 @@ static int accept_case(int argc_trials) {
   return g_bad ? 1 : 0;
 }
 
+// case 8: mc_accept_noalloc against mc_accept (no generated history) on the same inputs,
+// two calls in a row, the second smaller; caller uniforms on the second.
+template <class T>
+static T* dev_copy(const std::vector<T>& h) {
+  T* d = nullptr;
+  check(hipMalloc((void**)&d, h.size() * sizeof(T)) == hipSuccess ? 0 : -1, "hipMalloc");
+  check(hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) == hipSuccess ? 0 : -1, "copy");
+  return d;
+}
+
+static int noalloc_case() {
+  const int V = 3000;
+  const int shapes[2][2] = {{6, 5}, {3, 2}};  // (B, K)
+  for (int call = 0; call < 2; ++call) {
+    const int B = shapes[call][0], K = shapes[call][1], K1 = K + 1;
+    std::vector<int32_t> nd(B), dr((size_t)B * std::max(K, 1), 0);
+    std::vector<mc_sampling> sp(B);
+    std::vector<uint64_t> ctr(B);
+    std::vector<uint32_t> uni((size_t)B * K1 * 2);
+    for (auto& u : uni) u = (uint32_t)or_mix64(rng_state++);
+    std::vector<uint16_t> lg((size_t)B * K1 * V);
+    for (size_t i = 0; i < lg.size(); ++i) {
+      const int id = (int)(i % V);
+      lg[i] = or_f32_to_bf16(id < 12 ? (float)((int)rnd(12) + 6) * 0.5f : (float)((int)rnd(16) - 20) * 0.5f);
+    }
+    for (int r = 0; r < B; ++r) {
+      nd[r] = (int)rnd(K + 1);
+      for (int j = 0; j < nd[r]; ++j) {  // mostly the position's argmax: long accepted prefixes
+        const uint16_t* row = lg.data() + ((size_t)r * K1 + j) * V;
+        int am = 0;
+        for (int i = 1; i < V; ++i)
+          if (bf(row[i]) > bf(row[am])) am = i;
+        dr[(size_t)r * K + j] = rnd(4) ? am : (int)rnd(12);
+      }
+      mc_sampling q;
+      memset(&q, 0, sizeof q);
+      q.temperature = r % 2 ? 0.8f : 0.f;
+      q.top_p = r % 3 == 1 ? 0.9f : 0.f;
+      q.top_k = r == 3 ? 4 : 0;
+      q.presence_penalty = r == 2 ? 1.0f : 0.f;
+      q.n_bias = r == 4 ? 1 : 0;
+      q.bias_token[0] = 5;
+      q.bias_value[0] = 3.0f;
+      q.has_seed = 1;
+      q.seed = 900 + r;
+      q.reject_token = -1;
+      sp[r] = q;
+      ctr[r] = rnd(50);
+    }
+    // mc_accept over host buffers: row r's logits rows at r*K1 .. r*K1 + nd[r]
+    std::vector<int64_t> off(B + 1, 0);
+    std::vector<uint16_t> packed;
+    for (int r = 0; r < B; ++r) {
+      off[r + 1] = off[r] + nd[r] + 1;
+      packed.insert(packed.end(), lg.begin() + (size_t)r * K1 * V, lg.begin() + ((size_t)r * K1 + nd[r] + 1) * V);
+    }
+    const uint32_t* use_u = call == 1 ? uni.data() : nullptr;
+    std::vector<int32_t> want((size_t)B * K1, -7), wne(B), wkeep(B), wnacc(B);
+    check(mc_accept(packed.data(), V, B, off.data(), dr.data(), K, nd.data(), sp.data(), nullptr, nullptr, ctr.data(),
+                    use_u, 1, want.data(), wne.data(), wkeep.data(), wnacc.data()),
+          "mc_accept");
+    uint16_t* d_lg = dev_copy(lg);
+    int32_t* d_dr = dev_copy(dr);
+    int32_t* d_nd = dev_copy(nd);
+    uint32_t* d_u = dev_copy(uni);
+    std::vector<int32_t> zeros((size_t)B * K1, -7), zr(B, 0);
+    int32_t *d_out = dev_copy(zeros), *d_ne = dev_copy(zr), *d_keep = dev_copy(zr), *d_nacc = dev_copy(zr);
+    check(mc_accept_noalloc(d_lg, V, B, K, d_dr, d_nd, sp.data(), ctr.data(), call == 1 ? d_u : nullptr, 1, d_out, d_ne,
+                            d_keep, d_nacc),
+          "mc_accept_noalloc");
+    std::vector<int32_t> got((size_t)B * K1), ne(B), keep(B), nacc(B);
+    hipMemcpy(got.data(), d_out, got.size() * 4, hipMemcpyDeviceToHost);
+    hipMemcpy(ne.data(), d_ne, B * 4, hipMemcpyDeviceToHost);
+    hipMemcpy(keep.data(), d_keep, B * 4, hipMemcpyDeviceToHost);
+    hipMemcpy(nacc.data(), d_nacc, B * 4, hipMemcpyDeviceToHost);
+    for (int r = 0; r < B; ++r) {
+      bool same = ne[r] == wne[r] && keep[r] == wkeep[r] && nacc[r] == wnacc[r];
+      for (int j = 0; same && j < ne[r]; ++j) same = got[(size_t)r * K1 + j] == want[(size_t)r * K1 + j];
+      printf("call %d row %d: n %d keep %d acc %d %s\n", call, r, ne[r], keep[r], nacc[r], same ? "same" : "DIFFERENT");
+      if (!same) ++g_bad;
+    }
+    for (void* p : {(void*)d_lg, (void*)d_dr, (void*)d_nd, (void*)d_u, (void*)d_out, (void*)d_ne, (void*)d_keep,
+                    (void*)d_nacc})
+      hipFree(p);
+  }
+  printf("%s\n", g_bad ? "FAIL" : "OK");
+  return g_bad ? 1 : 0;
+}
+
 int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
   check(mc_set_device(0), "set_device");
   if (cs == 7) return accept_case(argc > 2 ? atoi(argv[2]) : 0);
+  if (cs == 8) return noalloc_case();
   mc_model_config c{};
   c.arch = 0; c.n_layers = 2; c.hidden = 256; c.n_q_heads = 4; c.n_kv_heads = 2; c.head_dim = 128;
   c.intermediate = 512; c.vocab = 4096; c.tied_embeddings = 1; c.rms_eps = 1e-6f; c.rope_theta = 1e6f;
