@@ -181,6 +181,13 @@ int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len);
 /* Copy one row's K (which_v = 0) or V (1) of one layer to host: [n_kv][len][d] bf16. */
 int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t which_v, uint16_t* out);
 int mc_batch_history(mc_batch* b, int32_t row, int32_t* out, int32_t cap, int32_t* len);
+/* The last layer's attention output (before o_proj) of the last forward, the first M of
+ * its token slots: out[M][n_q_heads * head_dim] bf16 (parity inspection, like
+ * mc_batch_read_kv; the slots of mc_forward are its rows' tokens in call order). */
+int mc_batch_read_attention(mc_batch* b, int32_t M, uint16_t* out);
+/* Logits of token slots [slot0, slot0 + n) of the last forward: out[n][vocab] bf16.  After
+ * mc_step, row r's verify position j is slot r * (K + 1) + j. */
+int mc_batch_read_logits(mc_batch* b, int32_t slot0, int32_t n, uint16_t* out);
 
 /* ---- forward: LanguageModel.callAsFunction(LMInput.Text, cache:, state:)
  * (BatchGenerator.swift:900-904).  counts[r] new tokens for each listed row, positions

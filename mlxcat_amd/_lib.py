@@ -25,7 +25,9 @@ EXPORTS = [
     "mc_last_error", "mc_set_device", "mc_model_create", "mc_model_destroy", "mc_model_init_synthetic",
     "mc_model_set_linear", "mc_model_get_linear", "mc_model_set_norm", "mc_batch_create", "mc_batch_destroy",
     "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
-    "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_history",
+    "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_read_attention",
+    "mc_batch_read_logits",
+    "mc_batch_history",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
     "mc_batch_set_profiling", "mc_batch_profile",
 ]
@@ -102,6 +104,8 @@ def load(path: str = LIB_PATH):
         "mc_batch_kv_len": (C.c_int, [P, I32, P]),
         "mc_batch_read_kv": (C.c_int, [P, I32, I32, I32, P]),
         "mc_batch_history": (C.c_int, [P, I32, P, I32, P]),
+        "mc_batch_read_attention": (C.c_int, [P, I32, P]),
+        "mc_batch_read_logits": (C.c_int, [P, I32, I32, P]),
         "mc_forward": (C.c_int, [P, I32, P, P, P, P]),
         "mc_ngram_propose": (C.c_int, [P, P, I32, I32, I32, P, I32, P, P]),
         "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, P, P, P, I32, P, P, P, P]),
@@ -279,6 +283,20 @@ class Batch:
         c = self.model.cfg
         out = np.zeros((c.n_kv_heads, self.kv_len(row), c.head_dim), dtype=np.uint16)
         _check(load().mc_batch_read_kv(self.h, layer, row, which_v, _p(out)))
+        return out
+
+    def read_attention(self, M: int) -> np.ndarray:
+        """The last layer's attention output of the last forward's first M slots [M][nq * d]."""
+        c = self.model.cfg
+        out = np.zeros((M, c.n_q_heads * c.head_dim), dtype=np.uint16)
+        _check(load().mc_batch_read_attention(self.h, M, _p(out)))
+        return out
+
+    def read_logits(self, slot0: int, n: int) -> np.ndarray:
+        """Logits [n][V] of token slots slot0.. of the last forward (after step(): row r's
+        position j is slot r * (K + 1) + j)."""
+        out = np.zeros((n, self.model.cfg.vocab), dtype=np.uint16)
+        _check(load().mc_batch_read_logits(self.h, slot0, n, _p(out)))
         return out
 
     def history(self, row: int) -> list[int]:

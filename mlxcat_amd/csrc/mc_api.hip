@@ -450,6 +450,7 @@ struct mc_batch {
   uint64_t unseeded = 0;
   bool forced_none = true;  // the device's forced accept-length schedule is all -1
   bool uniforms_on = false; // the device reads caller uniforms
+  int last_M = 0;           // token slots of the last forward (mc_batch_read_attention)
   int32_t* gen_cnt = nullptr;  // [R][V] generated-token counts (rows with penalties)
   // profiling
   bool profiling = false;
@@ -816,6 +817,7 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   const auto& c = m->cfg;
   const StepState& s = b->s;
   int rc;
+  b->last_M = m->fake ? 0 : M;
   if (m->fake) {
     if (lgn > 0) return launch_fake_logits(c.arch, s.slot_tok + lg0, lgn, c.vocab, b->logits + (size_t)lg0 * c.vocab, b->st);
     return MC_OK;
@@ -1201,6 +1203,27 @@ extern "C" int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t
   return MC_OK;
 }
 
+extern "C" int mc_batch_read_attention(mc_batch* b, int32_t M, uint16_t* out) {
+  if (!b || !out || M < 0) return fail(MC_E_INVALID, "read_attention: bad argument");
+  if (M > b->last_M) return fail(MC_E_STATE, "read_attention: the last forward had fewer token slots");
+  MC_HIP(hipSetDevice(b->m->device));
+  MC_HIP(hipStreamSynchronize(b->st));
+  const auto& c = b->m->cfg;
+  MC_HIP(hipMemcpy(out, b->att, (size_t)M * c.n_q_heads * c.head_dim * 2, hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
+extern "C" int mc_batch_read_logits(mc_batch* b, int32_t slot0, int32_t n, uint16_t* out) {
+  if (!b || !out || slot0 < 0 || n < 0) return fail(MC_E_INVALID, "read_logits: bad argument");
+  const int V = b->m->cfg.vocab;
+  const int M = b->m->fake ? b->R * b->K1 : b->last_M;
+  if (slot0 + n > M) return fail(MC_E_STATE, "read_logits: the last forward had fewer token slots");
+  MC_HIP(hipSetDevice(b->m->device));
+  MC_HIP(hipStreamSynchronize(b->st));
+  MC_HIP(hipMemcpy(out, b->logits + (size_t)slot0 * V, (size_t)n * V * 2, hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
 extern "C" int mc_batch_history(mc_batch* b, int32_t row, int32_t* out, int32_t cap, int32_t* len) {
   if (!b || !len) return fail(MC_E_INVALID, "null argument");
   int rc = check_row(b, row);
@@ -1282,6 +1305,7 @@ extern "C" int mc_step(mc_batch* b, const int32_t* forced_accept, const uint32_t
       MC_HIP(hipGraphInstantiate(&b->graph, g, nullptr, nullptr, 0));
     }
     MC_HIP(hipGraphLaunch(b->graph, b->st));
+    b->last_M = b->m->fake ? 0 : R * K1;  // the replayed forward's slots
   }
   const StepState& s = b->s;
   int32_t* h = b->h_out;

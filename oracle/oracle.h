@@ -180,6 +180,10 @@ int or_forward(or_model* m, int nrows, const int32_t* rows, const int32_t* count
  * hidden[(layer+1)][M][H] bf16 with hidden[0] = embeddings; NULL to skip. */
 int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t* counts,
                      const int32_t* tokens, uint16_t* logits, uint16_t* hidden);
+/* ... and each layer's attention output (before o_proj), attn[layer][M][n_q_heads * head_dim]
+ * bf16; NULL to skip. */
+int or_forward_attn(or_model* m, int nrows, const int32_t* rows, const int32_t* counts,
+                    const int32_t* tokens, uint16_t* logits, uint16_t* hidden, uint16_t* attn);
 
 void or_set_threads(int n);
 /* reversed != 0: every fp32 reduction of the forward (linears, RMSNorm, attention) runs in

@@ -323,6 +323,11 @@ static void fake_logits(const or_model* m, const int32_t* tokens, int M, uint16_
 
 int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t* counts,
                      const int32_t* tokens, uint16_t* logits, uint16_t* hidden) {
+  return or_forward_attn(m, nrows, rows, counts, tokens, logits, hidden, NULL);
+}
+
+int or_forward_attn(or_model* m, int nrows, const int32_t* rows, const int32_t* counts,
+                    const int32_t* tokens, uint16_t* logits, uint16_t* hidden, uint16_t* attn) {
   const or_config* c = &m->cfg;
   int M = 0;
   for (int i = 0; i < nrows; ++i) {
@@ -434,6 +439,8 @@ int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t*
         for (int i = 0; i < d; ++i) att[((size_t)t * nq + h) * d + i] = bf(tobf(acc[i] * inv));
         free(sc);
       }
+    if (attn)
+      for (size_t i = 0; i < (size_t)M * nq * d; ++i) attn[(size_t)l * M * nq * d + i] = tobf(att[i]);
     qlinear(&y->o, att, M, o);
     for (size_t i = 0; i < (size_t)M * H; ++i) x[i] = bf(tobf(x[i] + o[i]));
     for (int t = 0; t < M; ++t) rmsnorm(x + (size_t)t * H, y->post_norm, H, c->rms_eps, xn + (size_t)t * H);

@@ -106,6 +106,7 @@ def lib():
             "or_kv_read": (None, [P, I, I, I, P]),
             "or_forward": (I, [P, I, P, P, P, P]),
             "or_forward_trace": (I, [P, I, P, P, P, P, P]),
+            "or_forward_attn": (I, [P, I, P, P, P, P, P, P]),
             "or_set_threads": (None, [I]),
             "or_set_reduction_order": (None, [I]),
             "or_generator_create": (P, [P, P, I, I, U64]),
@@ -266,17 +267,22 @@ class Model:
         lib().or_kv_read(self.h, layer, row, which_v, _p(out))
         return out
 
-    def forward(self, rows, counts, tokens, want_logits=True, trace=False):
+    def forward(self, rows, counts, tokens, want_logits=True, trace=False, attention=False):
+        """Logits [M][V]; with trace=True also the hidden states, with attention=True also each
+        layer's attention output [layers][M][nq * d] (returned as a tuple in that order)."""
         rows, counts, tokens = i32(rows), i32(counts), i32(tokens)
         M = int(counts.sum())
-        lg = np.zeros((M, self.cfg.vocab), dtype=np.uint16) if want_logits else None
-        hid = np.zeros((self.cfg.n_layers + 1, M, self.cfg.hidden), dtype=np.uint16) if trace else None
-        rc = lib().or_forward_trace(self.h, len(rows), _p(rows), _p(counts), _p(tokens),
-                                    _p(lg) if lg is not None else None,
-                                    _p(hid) if hid is not None else None)
+        c = self.cfg
+        lg = np.zeros((M, c.vocab), dtype=np.uint16) if want_logits else None
+        hid = np.zeros((c.n_layers + 1, M, c.hidden), dtype=np.uint16) if trace else None
+        att = np.zeros((c.n_layers, M, c.n_q_heads * c.head_dim), dtype=np.uint16) if attention else None
+        rc = lib().or_forward_attn(self.h, len(rows), _p(rows), _p(counts), _p(tokens),
+                                   _p(lg) if lg is not None else None, _p(hid) if hid is not None else None,
+                                   _p(att) if att is not None else None)
         if rc:
             raise RuntimeError(f"or_forward failed: {rc}")
-        return (lg, hid) if trace else lg
+        out = [lg] + ([hid] if trace else []) + ([att] if attention else [])
+        return tuple(out) if len(out) > 1 else lg
 
 
 class reversed_reduction_order:
