@@ -230,7 +230,9 @@ int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uin
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-constexpr int FA_TP = 2;  // query tiles of 16 per pass
+// query tiles of 16 per pass over the keys: every tile of a (row, kv head) in one pass
+// (at most 4, 64 queries), so the keys and values are read once
+inline int attn_tiles(int nqry) { return std::min(4, std::max(1, (nqry + 15) / 16)); }
 
 // Merge of one query's split partials 0 .. ns - 1, in split order, for the output element
 // pair (e0, e0 + 1): running max, rescaled sums (the arithmetic of the standalone merge
@@ -282,10 +284,10 @@ __device__ inline float2 merge_splits(const float* pml, const float* po, int ns,
 // weights each split by exp(m_sp - M) / L in one pass (the standalone merge rescales a running
 // sum split by split), so attention outputs agree with the three-kernel path to rounding.
 
-template <int D, bool FUSE>
+template <int D, bool FUSE, int TP>
 __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLayer kv, SlotView sv, int nq, int nkv,
                                                          float scale, int S, AttnWork w, AttnFuse f) {
-  __shared__ float mrg[4][FA_TP][16][D + 2];  // per wave: o[d], max, sum of each query of the pass
+  __shared__ float mrg[4][TP][16][D + 2];  // per wave: o[d], max, sum of each query of the pass
   __shared__ __align__(16) uint16_t qs[FUSE ? FUSE_QMAX * D : 8];
   __shared__ int s_last;
   const int G = nq / nkv;
@@ -411,12 +413,12 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
     __syncthreads();  // the queries and this range's new keys are visible to every wave
   }
   const int nqt = (nqry + 15) / 16;
-  for (int t0 = 0; t0 < nqt; t0 += FA_TP) {
+  for (int t0 = 0; t0 < nqt; t0 += TP) {
     // B operands: q rows of queries (t0 + tt) 16 + r16, d = 32 s + 8 c .. + 7
-    bf16x8_t qb[FA_TP][4];
-    int qpos[FA_TP];
+    bf16x8_t qb[TP][4];
+    int qpos[TP];
 #pragma unroll
-    for (int tt = 0; tt < FA_TP; ++tt) {
+    for (int tt = 0; tt < TP; ++tt) {
       const int qi = min((t0 + tt) * 16 + r16, nqry - 1);
       const int j = qi / G, gh = qi - j * G;
       qpos[tt] = (t0 + tt) * 16 + r16 < nqry ? base + j : -1;
@@ -426,10 +428,10 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
         qb[tt][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(qp + 32 * s4 + 8 * c)
                              : __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
     }
-    float mrun[FA_TP], lrun[FA_TP];
-    f32x4_t o[FA_TP][NDB];
+    float mrun[TP], lrun[TP];
+    f32x4_t o[TP][NDB];
 #pragma unroll
-    for (int tt = 0; tt < FA_TP; ++tt) {
+    for (int tt = 0; tt < TP; ++tt) {
       mrun[tt] = -INFINITY;
       lrun[tt] = 0.f;
 #pragma unroll
@@ -438,7 +440,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
     for (int sc = sc_first; sc < s1; sc += 4 * ATTN_CHUNK) {
       if (!(pre && t0 == 0 && sc == sc_first)) load_kv(sc);
 #pragma unroll
-      for (int tt = 0; tt < FA_TP; ++tt) {
+      for (int tt = 0; tt < TP; ++tt) {
         if (t0 + tt >= nqt) break;
         f32x4_t st[4];
 #pragma unroll
@@ -500,7 +502,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
     }
     // ---- merge the four waves in wave order: one partial per (query, split) ----
 #pragma unroll
-    for (int tt = 0; tt < FA_TP; ++tt) {
+    for (int tt = 0; tt < TP; ++tt) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -511,9 +513,9 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
       }
     }
     __syncthreads();
-    // thread: query (tt, qq) = tid / 8 (FA_TP x 16 = 32 queries), d slice 16 (tid % 8)
-    {
-      const int qsel = threadIdx.x >> 3, part = threadIdx.x & 7;
+    // thread: query (tt, qq) = tid / 8 + 32 i (TP x 16 queries), d slice 16 (tid % 8)
+    for (int qsel = threadIdx.x >> 3; qsel < TP * 16; qsel += 32) {
+      const int part = threadIdx.x & 7;
       const int tt = qsel >> 4, qq = qsel & 15;
       const int qi = (t0 + tt) * 16 + qq;
       if (t0 + tt < nqt && qi < nqry) {
@@ -663,11 +665,23 @@ int attn_split(int R, int nkv, int nchunk, bool fused) {
 }
 
 bool attn_fuse_ok(int R, int nkv, int nchunk, int max_q, int nq, int d) {
-  if (max_q * (nq / nkv) > FUSE_QMAX) return false;
+  const int nqry = max_q * (nq / nkv);
+  if (nqry > FUSE_QMAX) return false;
   // the merging block keeps (m, l) per (query, split) and 1 / L per query in the pass buffer
-  const int S = attn_split(R, nkv, nchunk, true);
-  const size_t words = (size_t)FUSE_QMAX * (2 * ((nchunk + S - 1) / S) + 1);
-  return words <= (size_t)4 * FA_TP * 16 * (d + 2);
+  const int S = attn_split(R, nkv, nchunk, true), TP = attn_tiles(nqry);
+  const size_t words = (size_t)TP * 16 * (2 * ((nchunk + S - 1) / S) + 1);
+  return words <= (size_t)4 * TP * 16 * (d + 2);
+}
+
+template <int D, bool FUSE>
+static void launch_flash(int TP, dim3 grid, hipStream_t st, const uint16_t* q, const KVLayer& kv, const SlotView& sv,
+                         int nq, int nkv, float scale, int S, const AttnWork& w, const AttnFuse& f) {
+  switch (TP) {
+    case 1: hipLaunchKernelGGL((attn_flash_kernel<D, FUSE, 1>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f); break;
+    case 2: hipLaunchKernelGGL((attn_flash_kernel<D, FUSE, 2>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f); break;
+    case 3: hipLaunchKernelGGL((attn_flash_kernel<D, FUSE, 3>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f); break;
+    default: hipLaunchKernelGGL((attn_flash_kernel<D, FUSE, 4>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f); break;
+  }
 }
 
 int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, int max_q, int nq, int nkv, int d,
@@ -680,12 +694,13 @@ int launch_attention(const uint16_t* q, KVLayer kv, const SlotView& sv, int R, i
   const dim3 grid(R * nkv, (w.nchunk + S - 1) / S);
   const AttnFuse nf{};
   const AttnFuse& f = fuse ? *fuse : nf;
+  const int TP = attn_tiles(max_q * (nq / nkv));
   if (d == 128) {
-    if (fuse) hipLaunchKernelGGL((attn_flash_kernel<128, true>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
-    else hipLaunchKernelGGL((attn_flash_kernel<128, false>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    if (fuse) launch_flash<128, true>(TP, grid, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    else launch_flash<128, false>(TP, grid, st, q, kv, sv, nq, nkv, scale, S, w, f);
   } else {
-    if (fuse) hipLaunchKernelGGL((attn_flash_kernel<64, true>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
-    else hipLaunchKernelGGL((attn_flash_kernel<64, false>), grid, dim3(256), 0, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    if (fuse) launch_flash<64, true>(TP, grid, st, q, kv, sv, nq, nkv, scale, S, w, f);
+    else launch_flash<64, false>(TP, grid, st, q, kv, sv, nq, nkv, scale, S, w, f);
   }
   MC_HIP(hipGetLastError());
   if (fuse) return MC_OK;

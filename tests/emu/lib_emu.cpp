@@ -365,7 +365,7 @@ int main(int argc, char** argv) {
     or_forward(om, 1, &row0, &n, t.data(), nullptr);
     printf("prefill done\n");
   }
-  const std::vector<int> widths = cs == 2 ? std::vector<int>{6} : std::vector<int>{6, 1, 8};
+  const std::vector<int> widths = cs == 2 ? std::vector<int>{6} : cs == 3 ? std::vector<int>{6, 1, 8, 12, 16} : std::vector<int>{6, 1, 8};
   for (int w : widths) {
     auto t = tokens(w);
     std::vector<uint16_t> got((size_t)w * V), want((size_t)w * V);
