@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 QWEN3_4B = dict(arch=0, n_layers=36, hidden=2560, n_q_heads=32, n_kv_heads=8, head_dim=128, intermediate=9728,
                 vocab=151936, tied_embeddings=1, rms_eps=1e-6, rope_theta=1e6, n_experts=0, n_experts_per_tok=0,
                 moe_intermediate=0)
-K_DRAFT, MATCH, PROMPT_LEN, SEED = 5, 3, 2048, 1234
+K_DRAFT, MATCH, PROMPT_LEN, DECODE, SEED = 5, 3, 2048, 256, 1234
 # HBM bytes per launch of the verify GEMVs, measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
 # (scaled by the same counters over a plain 256 MiB copy); the commands are in the
 # summary beside this file
@@ -63,7 +63,13 @@ def step_bytes(cfg: dict, ctx_lens, M: int) -> float:
     return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
 
 
-def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
+def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = False):
+    """The 256-token decode of the workload: W warmup steps and an untimed prefix, then the
+    timed steps, placed so that the timed window ends near token 256 (the rows' budget is
+    256 plus the timed steps' worth, so no row finishes inside it).  forced: exactly L drafts
+    accepted per row per step, L uniform in [0, K], then the history's next token (the
+    survey's forced accept-length schedule: throughput at a known acceptance, whatever the
+    random-init weights agree with)."""
     from mlxcat_amd import _lib as hip
     from mlxcat_amd.workloads import copy_span_prompt
     L = hip.load()
@@ -71,34 +77,45 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool):
         raise RuntimeError(L.mc_last_error().decode())
     m = hip.Model(QWEN3_4B)
     m.init_synthetic(SEED)
-    max_new = (warmup + steps + 8) * (K_DRAFT + 1) + 8
+    rng = np.random.default_rng(SEED + 17)
+    max_new = DECODE + (steps + 1) * (K_DRAFT + 1)
     ctx = PROMPT_LEN + max_new + K_DRAFT + 16
     b = hip.Batch(m, rows, ctx, spec_cfg(rows))
+    generated = np.ones(rows, dtype=np.int64)  # the first token, sampled at admission
     for r in range(rows):
         p = copy_span_prompt(SEED + r, PROMPT_LEN, QWEN3_4B["vocab"])
         b.insert(r, p, max_new, hip.make_sampling())
+    fa = (lambda: rng.integers(0, K_DRAFT + 1, rows).astype(np.int32)) if forced else (lambda: None)
     for _ in range(warmup):
-        b.step()
+        generated += b.step(fa())[1]
+    # untimed prefix: until the timed steps at the warm-up rate end at token DECODE
+    rate = max(1.0, (generated.min() - 1) / max(1, warmup))
+    prefix = 0
+    while generated.min() < DECODE - steps * rate and prefix < 4 * DECODE:
+        generated += b.step(fa())[1]
+        prefix += 1
     st0 = b.stats()
     kv0 = [b.kv_len(r) for r in range(rows)]
     emitted = 0
     t0 = time.perf_counter()
     for _ in range(steps):
-        _, c, _ = b.step()
+        _, c, _ = b.step(fa())
         emitted += int(c.sum())
+        generated += c
     dt = time.perf_counter() - t0
     st1 = b.stats()
     out = dict(tok_s=emitted / dt, ms_per_step=dt / steps * 1e3, tokens_per_step=emitted / steps / rows,
                proposed=st1["proposed"] - st0["proposed"], accepted=st1["accepted"] - st0["accepted"],
                batches=st1["proposal_batches"] - st0["proposal_batches"],
-               bytes_per_step=step_bytes(QWEN3_4B, kv0, rows * (K_DRAFT + 1)))
+               bytes_per_step=step_bytes(QWEN3_4B, kv0, rows * (K_DRAFT + 1)),
+               timed_tokens=[int(generated.min() - emitted // rows), int(generated.max())], prefix_steps=prefix)
     out["step_hbm_gbs"] = out["bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
     if profile:
         # kind 0: the dequant GEMVs of the verify forward, timed with HIP events on the batch stream
         b.set_profiling(True)
         acc = [0.0, 0.0, 0]
         for _ in range(3):
-            b.step()
+            b.step(fa())
             ms, by, n = b.profile(0)
             acc[0] += ms
             acc[1] += by
@@ -184,19 +201,30 @@ def run_config(name: str, steps: int, warmup: int) -> dict:
             "dtype": "bf16", "data": "synthetic (random-init weights, synthetic K/V, seeded copy-span prompts)"}
 
 
-def run_cpu(budget_s: float = 20.0):
-    """The oracle (CPU restatement, OpenMP) on a bounded sample of the same batch-1 step:
-    synthetic K/V for the 2047 prefilled positions, then speculative steps until the
-    time budget is spent."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_cpu(rows: int = 1, budget_s: float = 15.0):
+    """The oracle (CPU restatement, OpenMP) on a bounded sample of the same step: synthetic
+    K/V for each row's 2047 prefilled positions, then speculative steps until the time
+    budget is spent."""
     from mlxcat_amd.workloads import copy_span_prompt
     from oracle import pyoracle as O
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     O.lib().or_set_threads(threads)
-    p = copy_span_prompt(SEED, PROMPT_LEN, QWEN3_4B["vocab"])
-    om = O.Model(QWEN3_4B, SEED, PROMPT_LEN + 128, 1)
-    om.fill_kv(0, PROMPT_LEN - 1, 99)
-    g = O.Generator(om, spec_cfg(1), 1, PROMPT_LEN + 128)
-    g.insert_prefilled(0, p, 100, O.make_sampling())
+    om = O.Model(QWEN3_4B, SEED, PROMPT_LEN + 128, rows)
+    g = O.Generator(om, spec_cfg(rows), rows, PROMPT_LEN + 128)
+    for r in range(rows):
+        om.fill_kv(r, PROMPT_LEN - 1, 99 + r)
+        g.insert_prefilled(r, copy_span_prompt(SEED + r, PROMPT_LEN, QWEN3_4B["vocab"]), 100, O.make_sampling())
     g.step()  # warm-up
     n_steps = emitted = 0
     t0 = time.perf_counter()
@@ -206,9 +234,9 @@ def run_cpu(budget_s: float = 20.0):
         n_steps += 1
     dt = time.perf_counter() - t0
     om.close()
-    return dict(value=emitted / dt, unit="tok/s", cores=threads, kind="port",
-                sample=f"{n_steps} speculative steps of the batch-1 Qwen3-4B-shape K=5 workload "
-                       f"({emitted} tokens, {dt:.1f} s) after a synthetic 2047-position KV prefill")
+    return dict(value=emitted / dt, unit="tok/s", cores=threads, kind="port", cpu_model=cpu_model(),
+                sample=f"{n_steps} speculative steps of the batch-{rows} Qwen3-4B-shape K=5 workload "
+                       f"({emitted} tokens, {dt:.1f} s) after a synthetic 2047-position KV prefill per row")
 
 
 def main():
@@ -246,8 +274,12 @@ def main():
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
     b1 = run_gpu(1, a.steps, a.warmup, profile=True)
+    b1f = run_gpu(1, a.steps, a.warmup, profile=False, forced=True)
     b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False)
-    cpu = None if a.no_cpu else run_cpu()
+    cpu = None if a.no_cpu else run_cpu(1)
+    cpu8 = None if (a.no_cpu or a.no_b8) else run_cpu(8, budget_s=10.0)
+    if cpu is not None and cpu8 is not None:
+        cpu["batch8"] = {k: cpu8[k] for k in ("value", "unit", "sample")}
     g = b1["dominant"]
     achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
     line = {
@@ -264,7 +296,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (random-init MLX 4-bit affine g64 weights, seeded copy-span prompts)",
         "config": {"workload": "Qwen3-4B-shape 4-bit g64 n-gram speculative step, batch 1, K=5, match 3, "
-                               "2048-token prompt, greedy", "batch": 1, "k_draft": K_DRAFT, "prompt": PROMPT_LEN},
+                               "2048-token prompt, greedy, 256-token decode", "batch": 1, "k_draft": K_DRAFT,
+                   "prompt": PROMPT_LEN, "decode": DECODE, "timed_tokens": b1["timed_tokens"]},
         "tokens_per_step": round(b1["tokens_per_step"], 3),
         "draft_hit_rate": round(b1["batches"] / a.steps, 3),
         "accepted_drafts_per_step": round(b1["accepted"] / a.steps, 3),
@@ -277,6 +310,13 @@ def main():
                      "kernel": g["kernel"], "launches_per_step": g["launches"],
                      "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 3),
                      "alg_bytes_per_launch": round(g["bytes"] / max(1, g["launches"]))},
+        "forced_accept": {"schedule": "exactly L ~ U[0, K] drafts accepted per step, then the history's next token "
+                                      "(a stress of the speculative mechanics: the row keeps copying its history, "
+                                      "so every step proposes; the tokens are not the model's)",
+                          "tok_s": round(b1f["tok_s"], 2),
+                          "ms_per_step": round(b1f["ms_per_step"], 4),
+                          "tokens_per_step": round(b1f["tokens_per_step"], 3),
+                          "accepted_drafts_per_step": round(b1f["accepted"] / a.steps, 3)},
         "batch8": None if b8 is None else {"tok_s": round(b8["tok_s"], 2), "ms_per_step": round(b8["ms_per_step"], 4),
                                            "tokens_per_step_per_row": round(b8["tokens_per_step"], 3),
                                            "step_hbm_frac": round(b8["step_hbm_gbs"] / HBM_PEAK_GBS, 4)},

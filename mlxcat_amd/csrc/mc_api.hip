@@ -614,7 +614,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
                o_sca = take(RK), o_scr = take(RK), o_forced = take(R), o_stats = take(8),
                o_topk = take(R), o_mpl = take(R), o_rp = take(R), o_pp = take(R), o_fp = take(R),
                o_mint = take(R), o_nb = take(R), o_bt = take(16 * R), o_bv = take(16 * R), o_proc = take(R),
-               o_uni = take(2 * RK), o_useu = take(2),
+               o_uni = take(2 * RK), o_useu = take(2), o_dext = take(R),
                // what a step returns, contiguous so that one copy brings it to the host:
                // [RK tokens | R counts | R finish | R proposal lengths | R KV lengths]
                o_otok = take(RK + 4 * R), o_ocnt = o_otok + RK, o_ofin = o_ocnt + R, o_np = o_ofin + R,
@@ -637,7 +637,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   s.top_k = I32(o_topk); s.min_p_log = F32(o_mpl); s.rep_pen = F32(o_rp); s.pres_pen = F32(o_pp);
   s.freq_pen = F32(o_fp); s.min_tokens = I32(o_mint); s.n_bias = I32(o_nb); s.bias_tok = I32(o_bt);
   s.bias_val = F32(o_bv); s.proc = I32(o_proc);
-  s.uniforms = reinterpret_cast<const uint32_t*>(base + o_uni); s.use_uniforms = I32(o_useu);
+  s.uniforms = reinterpret_cast<const uint32_t*>(base + o_uni); s.use_uniforms = I32(o_useu); s.dext = I32(o_dext);
   if ((rc = dev_zero(&b->gen_cnt, R * (size_t)V))) { batch_free(b); return rc; }
   s.gen_cnt = b->gen_cnt;
   if (!m->fake) { s.amax = b->amax; s.amax_nt = m->head().NT; }

@@ -73,10 +73,17 @@ __global__ void __launch_bounds__(256) propose_kernel(StepState s) {
         const int e = ngram_best_end(ctx, n, s.max_suffix, s.min_ctx, red);
         if (e > 0) P = min(limit, n - e);
         if (P > 0 && tid < P) s.drafts[r * s.K1 + tid] = ctx[e + tid];
+        // the continuation token after the drafts (the forced schedule's correction)
+        if (P > 0 && tid == 0 && s.dext) {
+          const bool ext = e + P < n;
+          s.dext[r] = ext ? 1 : 0;
+          if (ext) s.drafts[r * s.K1 + P] = ctx[e + P];
+        }
       }
     }
   }
   if (tid == 0) {
+    if (P == 0 && s.dext) s.dext[r] = 0;
     s.nprop[r] = act ? P : 0;
     s.n_valid[r] = act ? P + 1 : 0;
     s.row_slot0[r] = r * s.K1;
@@ -512,11 +519,13 @@ __global__ void __launch_bounds__(SCAN_THREADS) accept_scan_kernel(StepState s, 
   const uint32_t* uu = caller_u ? s.uniforms + ((size_t)r * s.K1 + j) * 2 : nullptr;
   const uint32_t u_acc = caller_u ? uu[0] : uniform_u32(seed, ctr, (uint32_t)j, 0u);
   const uint32_t u_smp = caller_u ? uu[1] : uniform_u32(seed, ctr, (uint32_t)j, 1u);
+  const bool forced = s.forced && s.forced[r] >= 0;  // the draw after forced drafts excludes nothing
   if (j < P) {
     const int x = s.drafts[r * s.K1 + j];
     const uint64_t wx = tmass(d, pv(x), x, inv_t);
     const int acc = mulhi32(u_acc, d.total) < wx;
-    const int res = dist_sample_dev(d, pv, V, inv_t, u_smp, x, wx, red, s_int);
+    const int res = forced ? dist_sample_dev(d, pv, V, inv_t, u_smp, -1, 0, red, s_int)
+                           : dist_sample_dev(d, pv, V, inv_t, u_smp, x, wx, red, s_int);
     if (threadIdx.x == 0) {
       s.scan_acc[r * s.K1 + j] = acc;
       s.scan_res[r * s.K1 + j] = res;
@@ -582,19 +591,33 @@ __device__ int decide_row(const StepState& s, int r, int32_t* out, int* keep, in
         *nacc = na > 1 ? na - 1 : 0;                            // :952
       }
     }
+  } else if (s.forced && s.forced[r] >= 0) {
+    // forced accept-length schedule (stress workloads): exactly min(f, P) drafts count as
+    // accepted, up to an EOS or reject token among them, then the history's continuation
+    // token after them (the next draft, or the one after the last draft), or the model's
+    // token at that position when the history has none (sampled rows: drawn without
+    // exclusion)
+    int a = min(s.forced[r], P);
+    bool stop = false;
+    for (int pos = 0; pos < a; ++pos) {
+      const int t = dr[pos];
+      out[n++] = t;
+      if (t == rej || is_eos(s, r, t)) { a = pos + 1; stop = true; break; }
+    }
+    if (!stop) out[n++] = (a < P || (P > 0 && s.dext[r])) ? dr[a] : (greedy ? st[a] : sr[a]);
+    *keep = a + 1;
+    *nacc = a;
+    *rejected = (P > 0 && a < P) ? 1 : 0;
   } else {
-    int cap = P;
-    const int f = s.forced ? s.forced[r] : -1;
-    if (f >= 0 && f < cap) cap = f;
     int a = 0;
     bool stop = false;
     for (int pos = 0; pos < P; ++pos) {
       int t;
       if (greedy) {
         t = st[pos];
-        if (pos >= cap || t != dr[pos] || t == rej) { out[n++] = t; stop = true; break; }
+        if (t != dr[pos] || t == rej) { out[n++] = t; stop = true; break; }
       } else {
-        if (!(pos < cap && sa[pos])) { out[n++] = sr[pos]; stop = true; break; }
+        if (!sa[pos]) { out[n++] = sr[pos]; stop = true; break; }
         t = dr[pos];
       }
       out[n++] = t;

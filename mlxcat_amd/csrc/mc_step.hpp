@@ -48,6 +48,7 @@ struct StepState {
   // step scratch
   int32_t* drafts = nullptr;    // [R][K1]
   int32_t* nprop = nullptr;     // [R]
+  int32_t* dext = nullptr;      // [R] 1: drafts[r][nprop] holds the history's next token (forced schedule)
   int32_t* slot_tok = nullptr;  // [R * K1] (or larger for prefill)
   int32_t* slot_row = nullptr;
   int32_t* slot_pos = nullptr;

@@ -126,14 +126,20 @@ int or_process_logits(const uint16_t* lg, int V, const struct or_sampling* sp, c
  * rejection falls back to a one-token decode whose logits are position 0); rows with
  * temperature > 0 use speculative sampling with the uniforms of (seed, counter), or the
  * caller's: uniforms[j][0] the accept test and uniforms[j][1] the sample draw of position
- * j (NULL = derived).  forced_cap >= 0 caps the accepted drafts (forced accept-length
- * schedule), -1 = none.  Writes the emitted tokens to out and returns their count;
+ * j (NULL = derived).  forced_cap >= 0 (a forced accept-length schedule, stress workloads)
+ * accepts exactly min(forced_cap, P) drafts whatever the model says, up to an EOS or reject
+ * token among them, then emits the history's continuation token after them: the next draft,
+ * or dr[P] when all were accepted and has_ext says the history holds one, else the model's
+ * token at that position (sampled rows draw it without exclusion); -1 = none.  A row that
+ * keeps copying its history keeps proposing, so the schedule sets the accepted lengths
+ * whatever the weights.  Writes the emitted tokens to out and returns their count;
  * *kv_keep = verified positions kept in the KV, *n_acc = drafts accepted (the
  * SpeculativeDecodingStats increment, :952), *rejected = 1 when a proposal was (partly)
  * rejected (:938). */
 int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const struct or_sampling* sp,
                   const int32_t* gen, int n_gen, uint64_t seed, uint64_t counter, const uint32_t* uniforms,
-                  int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc, int* rejected);
+                  int acceptance, int forced_cap, int has_ext, int32_t* out, int* kv_keep, int* n_acc,
+                  int* rejected);
 
 /* ---- KV trim known answer: BatchCache.swift:403-424 ---- */
 /* Uniform trim of a left-padded batch: returns trimmed count, updates idx,

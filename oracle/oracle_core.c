@@ -358,7 +358,8 @@ static uint32_t draw(const uint32_t* uniforms, uint64_t seed, uint64_t counter, 
 
 int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_sampling* sp,
                   const int32_t* gen, int n_gen, uint64_t seed, uint64_t counter, const uint32_t* uniforms,
-                  int acceptance, int forced_cap, int32_t* out, int* kv_keep, int* n_acc, int* rejected) {
+                  int acceptance, int forced_cap, int has_ext, int32_t* out, int* kv_keep, int* n_acc,
+                  int* rejected) {
   const int sampled = sp->temperature != 0.0f;
   const float inv_t = sampled ? 1.0f / sp->temperature : 0.0f;
   const float lmp = or_min_p_log(sp->min_p);
@@ -399,19 +400,48 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
     free(v); free(gbuf);
     return na;
   }
+  if (forced_cap >= 0) {
+    /* forced accept-length schedule (stress workloads): exactly min(forced_cap, P) drafts
+     * count as accepted whatever the model says (up to an EOS or reject token among them),
+     * then the history's continuation token after them (dr[a]: the next draft, or when all
+     * P were accepted the extension dr[P] if has_ext), else the model's token at the next
+     * position, drawn without exclusion */
+    int a = forced_cap < P ? forced_cap : P, stop = 0;
+    for (int pos = 0; pos < a; ++pos) {
+      out[n_emit++] = dr[pos];
+      if (dr[pos] == sp->reject_token || is_eos_tok(sp, dr[pos])) { a = pos + 1; stop = 1; break; }
+    }
+    if (!stop && (a < P || (P > 0 && has_ext))) {
+      out[n_emit++] = dr[a];
+      stop = 1;
+    }
+    if (!stop) {
+      VALUES(a);
+      if (sampled) {
+        or_dist d;
+        or_dist_build_f(v, V, sp->temperature, sp->top_p, sp->top_k, lmp, &d);
+        out[n_emit++] = or_dist_sample_f(&d, v, V, inv_t, draw(uniforms, seed, counter, a, 1), -1);
+      } else {
+        out[n_emit++] = argmax_f(v, V);
+      }
+    }
+    *kv_keep = a + 1;
+    *n_acc = a;
+    *rejected = (P > 0 && a < P) ? 1 : 0;
+    free(v);
+    free(gbuf);
+    return n_emit;
+  }
   /* prefix acceptance (greedy) and speculative sampling (temperature > 0): accept drafts
    * while they agree, emit the correction (or the bonus token after a full accept), keep
-   * the current token + accepted drafts in the KV.  forced_cap >= 0 caps the accepted
-   * drafts (forced accept-length schedule). */
-  int cap = P;
-  if (forced_cap >= 0 && forced_cap < cap) cap = forced_cap;
+   * the current token + accepted drafts in the KV. */
   int a = 0, stop = 0;
   for (int pos = 0; pos < P; ++pos) {
     VALUES(pos);
     int tok;
     if (!sampled) {
       tok = argmax_f(v, V);
-      if (pos >= cap || tok != dr[pos] || tok == sp->reject_token) {
+      if (tok != dr[pos] || tok == sp->reject_token) {
         out[n_emit++] = tok;
         stop = 1;
         break;
@@ -419,7 +449,7 @@ int or_accept_row(const uint16_t* lg, int V, const int32_t* dr, int P, const or_
     } else {
       or_dist d;
       or_dist_build_f(v, V, sp->temperature, sp->top_p, sp->top_k, lmp, &d);
-      const int ok = pos < cap && accept_draft(&d, v, inv_t, dr[pos], draw(uniforms, seed, counter, pos, 0));
+      const int ok = accept_draft(&d, v, inv_t, dr[pos], draw(uniforms, seed, counter, pos, 0));
       if (!ok) {
         out[n_emit++] = or_dist_sample_f(&d, v, V, inv_t, draw(uniforms, seed, counter, pos, 1), dr[pos]);
         stop = 1;
@@ -570,7 +600,7 @@ int or_generator_insert(or_generator* g, int row, const int32_t* prompt, int n_p
   rw->seed = sp->has_seed ? sp->seed : or_mix64(g->global_seed ^ or_mix64(++g->unseeded_count));
   rw->counter = 0;
   int tok, keep, nacc, rej;
-  or_accept_row(lg, V, NULL, 0, sp, NULL, 0, rw->seed, rw->counter, NULL, g->cfg.acceptance, -1, &tok, &keep, &nacc,
+  or_accept_row(lg, V, NULL, 0, sp, NULL, 0, rw->seed, rw->counter, NULL, g->cfg.acceptance, -1, 0, &tok, &keep, &nacc,
                 &rej);
   rw->counter++;
   free(lg);
@@ -625,8 +655,9 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
   if (n_active == 0) return 0;
   int32_t* rows = (int32_t*)malloc(sizeof(int32_t) * (size_t)R);
   int32_t* counts = (int32_t*)malloc(sizeof(int32_t) * (size_t)R);
-  int32_t* drafts = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * (size_t)(K + 1));
+  int32_t* drafts = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * (size_t)(K + 2));
   int32_t* nprop = (int32_t*)calloc((size_t)R, sizeof(int32_t));
+  int* ext = (int*)calloc((size_t)R, sizeof(int));
   int32_t* toks = (int32_t*)malloc(sizeof(int32_t) * (size_t)R * (size_t)(K + 1));
   int nr = 0, M = 0;
   for (int r = 0; r < R; ++r) {
@@ -638,9 +669,12 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
       if (remaining < 0) remaining = 0;
       if (remaining > 1) {                                                   /* :878 */
         int limit = K < remaining - 1 ? K : remaining - 1;                   /* :883 */
-        if (limit > 0)
+        if (limit > 0) {  /* one more token: the continuation after the drafts (forced schedule) */
           P = or_ngram_propose(rw->hist, rw->hist_len, g->cfg.max_suffix_tokens,
-                               g->cfg.min_context_tokens, limit, drafts + (size_t)r * (K + 1));
+                               g->cfg.min_context_tokens, limit + 1, drafts + (size_t)r * (K + 2));
+          ext[r] = P > limit;
+          if (P > limit) P = limit;
+        }
       }
     }
     nprop[r] = P;
@@ -648,14 +682,14 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
     rows[nr] = r;
     counts[nr] = P + 1;
     toks[M] = rw->cur;                                                       /* :897 */
-    for (int j = 0; j < P; ++j) toks[M + 1 + j] = drafts[(size_t)r * (K + 1) + j];
+    for (int j = 0; j < P; ++j) toks[M + 1 + j] = drafts[(size_t)r * (K + 2) + j];
     if (or_kv_len(g->m, r) > 0) record_width(g, P + 1);
     M += P + 1;
     nr++;
   }
   uint16_t* lg = (uint16_t*)malloc(2 * (size_t)M * (size_t)V);
   if (or_forward(g->m, nr, rows, counts, toks, lg)) {
-    free(rows); free(counts); free(drafts); free(nprop); free(toks); free(lg);
+    free(rows); free(counts); free(drafts); free(nprop); free(ext); free(toks); free(lg);
     return -1;
   }
   int produced = 0;
@@ -665,9 +699,10 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
     int32_t* out = out_tokens + (size_t)r * (K + 1);
     int kv_keep = 1, n_acc = 0, rejected = 0, n_gen = 0;
     const int32_t* gen = generated_of(rw, &n_gen);
-    const int n_emit = or_accept_row(lg + (size_t)t0 * V, V, drafts + (size_t)r * (K + 1), P, &rw->sp, gen, n_gen,
+    const int n_emit = or_accept_row(lg + (size_t)t0 * V, V, drafts + (size_t)r * (K + 2), P, &rw->sp, gen, n_gen,
                                      rw->seed, rw->counter, NULL, g->cfg.acceptance,
-                                     forced_accept ? forced_accept[r] : -1, out, &kv_keep, &n_acc, &rejected);
+                                     forced_accept ? forced_accept[r] : -1, ext[r], out, &kv_keep, &n_acc,
+                                     &rejected);
     if (P > 0) {
       g->stats.accepted += n_acc;                                     /* :952 */
       g->stats.rejected_batches += rejected;                          /* :938 */
@@ -690,7 +725,7 @@ int or_generator_step(or_generator* g, int32_t* out_tokens, int32_t* out_counts,
     if (fin) rw->active = 0;                                              /* Scheduler.swift:413-427 */
     produced++;
   }
-  free(rows); free(counts); free(drafts); free(nprop); free(toks); free(lg);
+  free(rows); free(counts); free(drafts); free(nprop); free(ext); free(toks); free(lg);
   return produced;
 }
 

@@ -93,7 +93,7 @@ def lib():
             "or_min_p_log": (F, [F]),
             "or_process_logits": (I, [P, I, P, P, I, P]),
             "or_batch_trim": (I, [P, I, P, P, I]),
-            "or_accept_row": (I, [P, I, P, I, P, P, I, U64, U64, P, I, I, P, P, P, P]),
+            "or_accept_row": (I, [P, I, P, I, P, P, I, U64, U64, P, I, I, I, P, P, P, P]),
             "or_qmatmul": (None, [P, P, P, I, I, P, I, P]),
             "or_model_create": (P, [P, U64, I, I]),
             "or_model_destroy": (None, [P]),
@@ -174,12 +174,13 @@ def qmatmul(wq, s, b, x) -> np.ndarray:
 
 
 def accept_row(logits_bf16: np.ndarray, drafts, sampling: "Sampling", seed: int, counter: int, acceptance: int,
-               forced_cap: int = -1, generated=(), uniforms=None):
+               forced_cap: int = -1, generated=(), uniforms=None, ext=None):
     """Acceptance of one row: logits_bf16 [P+1][V] uint16, drafts P tokens, `generated` the
     request's generated tokens so far, `uniforms` [P+1][2] caller draws (None = derived).
+    `ext`: the history's token after the drafts (the forced schedule's continuation), or None.
     Returns (emitted tokens, kv_keep, n_accepted, rejected)."""
     lg = np.ascontiguousarray(logits_bf16, dtype=np.uint16)
-    dr = i32(drafts) if len(drafts) else np.zeros(1, dtype=np.int32)
+    dr = i32(list(drafts) + ([ext] if ext is not None else [0]))
     P = len(drafts)
     assert lg.shape[0] == P + 1
     gen = i32(generated) if len(generated) else np.zeros(1, dtype=np.int32)
@@ -190,8 +191,8 @@ def accept_row(logits_bf16: np.ndarray, drafts, sampling: "Sampling", seed: int,
     out = np.zeros(P + 1, dtype=np.int32)
     keep, nacc, rej = C.c_int(), C.c_int(), C.c_int()
     n = lib().or_accept_row(_p(lg), lg.shape[1], _p(dr), P, C.byref(sampling), _p(gen), len(generated), seed,
-                            counter, _p(u) if u is not None else None, acceptance, forced_cap, _p(out),
-                            C.byref(keep), C.byref(nacc), C.byref(rej))
+                            counter, _p(u) if u is not None else None, acceptance, forced_cap,
+                            1 if ext is not None else 0, _p(out), C.byref(keep), C.byref(nacc), C.byref(rej))
     return out[:n].tolist(), keep.value, nacc.value, rej.value
 
 

@@ -133,7 +133,7 @@ static int accept_case(int argc_trials) {
       int wk, wn, wr;
       const int n = or_accept_row(lg.data() + (size_t)off[r] * V, V, dr.data() + (size_t)r * KD, nd[r], &osp[r],
                                   gen.data() + goff[r], (int)(goff[r + 1] - goff[r]), sp[r].seed, ctr[r],
-                                  use_u ? uni.data() + (size_t)r * (KD + 1) * 2 : nullptr, trial % 3 == 0 ? 0 : 1, -1,
+                                  use_u ? uni.data() + (size_t)r * (KD + 1) * 2 : nullptr, trial % 3 == 0 ? 0 : 1, -1, 0,
                                   want.data(), &wk, &wn, &wr);
       bool same = n == ne[r] && wk == keep[r] && wn == nacc[r];
       for (int j = 0; same && j < n; ++j) same = want[j] == out[(size_t)r * (KD + 1) + j];

@@ -89,9 +89,10 @@ def test_many_subchunks_llama3_8b(hip, oracle):
 def test_cfg5_shaped_step(hip, oracle):
     """32 rows x (K = 8) + 1 = 288 verify slots at the Qwen3-8B layer shapes (one layer, a
     4096-token vocabulary), even rows greedy, odd rows seeded (T 0.8, top-p 0.95), a forced
-    accept-length schedule, through mc_step on synthetic 1K-token contexts.
+    accept-length schedule (exactly L drafts accepted, then the history's next token),
+    through mc_step on synthetic 1K-token contexts.
     - Every row's emitted tokens equal or_accept_row on the step's own verify logits, bit for
-      bit (sampled rows also equal mc_accept on them).
+      bit, and mc_accept's speculative sampling on those logits equals or_accept_row's.
     - The step's logits are within the full-width bound of the oracle's forward of the same
       verify blocks, and greedy rows whose every used position has a clear top-2 margin emit
       what the oracle's acceptance emits on the oracle's logits."""
@@ -120,25 +121,27 @@ def test_cfg5_shaped_step(hip, oracle):
         gb.insert_prefilled(r, p, 64, sps[r])
     forced = rng.integers(0, K + 1, R).tolist()
     toks, counts, fins = gb.step(forced)
-    blocks, drafts = [], []
+    blocks, drafts, exts = [], [], []
     for r in range(R):
-        d = oracle.ngram_propose(prompts[r], 3, 8, K)
-        drafts.append(d)
-        blocks.append([prompts[r][-1]] + d)
+        d = oracle.ngram_propose(prompts[r], 3, 8, K + 1)  # + the history's next token
+        drafts.append(d[:K])
+        exts.append(d[K] if len(d) > K else None)
+        blocks.append([prompts[r][-1]] + d[:K])
     assert sum(len(d) for d in drafts) > 4 * R  # the repeated tails give proposals
     gpu_lg = [gb.read_logits(r * (K + 1), len(blocks[r])) for r in range(R)]
     # the step's acceptance on its own logits
     for r in range(R):
         want, keep, nacc, _ = oracle.accept_row(gpu_lg[r], drafts[r], osps[r], 700 + r, 0, 1, forced_cap=forced[r],
-                                                generated=[prompts[r][-1]])
+                                                generated=[prompts[r][-1]], ext=exts[r])
         assert toks[r, :counts[r]].tolist() == want, r
+    # the sampled rows' speculative sampling on the same logits (no forced schedule) through
+    # mc_accept, against or_accept_row
     odd = list(range(1, R, 2))
-    got, _, _ = hip.accept([gpu_lg[r] for r in odd], [drafts[r] for r in odd], [sps[r] for r in odd], [0] * len(odd),
-                           1)
+    got, keep, nacc = hip.accept([gpu_lg[r] for r in odd], [drafts[r] for r in odd], [sps[r] for r in odd],
+                                 [0] * len(odd), 1)
     for i, r in enumerate(odd):
-        cap = min(forced[r], len(drafts[r]))
-        if cap == len(drafts[r]):  # no forced cap below the proposal: mc_accept applies the same rule
-            assert got[i] == toks[r, :counts[r]].tolist(), r
+        want, wkeep, wnacc, _ = oracle.accept_row(gpu_lg[r], drafts[r], osps[r], 700 + r, 0, 1)
+        assert (got[i], keep[i], nacc[i]) == (want, wkeep, wnacc), r
     # the forward against the oracle's
     want_lg = om.forward(list(range(R)), [len(b) for b in blocks], [t for b in blocks for t in b])
     assert_close_bf16_wide(np.concatenate(gpu_lg), want_lg, what="cfg5-shaped verify logits")
@@ -146,7 +149,7 @@ def test_cfg5_shaped_step(hip, oracle):
     compared = 0
     for r in range(0, R, 2):
         w = want_lg[off[r]:off[r + 1]]
-        want, _, _, _ = oracle.accept_row(w, drafts[r], osps[r], 0, 0, 1, forced_cap=forced[r])
+        want, _, _, _ = oracle.accept_row(w, drafts[r], osps[r], 0, 0, 1, forced_cap=forced[r], ext=exts[r])
         used = max(len(want), int(counts[r]))  # verify positions either side's decision read
         vals = bf16_to_f32(w[:used]).astype(np.float64)
         if any(top2_margin(w[j]) <= 2 * (ATOL + RTOL * abs(vals[j].max())) for j in range(used)):
