@@ -57,6 +57,13 @@ __device__ inline void lds_barrier() {
 // 16 lanes that read one k-slot block from 16 different rows spread over banks.
 __host__ __device__ constexpr int xrow_stride(int kr) { return kr * 128 + 8; }
 
+// A raw buffer over n bytes at p: a load at an offset past n returns zero (the hardware's
+// range check), so a masked-off load needs no branch and no wait of its own.
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, int n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
+}
+constexpr unsigned NOWHERE = 0x80000000u;  // a buffer offset past every range used here
+
 constexpr int GEMV_WAVES = 4;
 constexpr int GEMV_LDS_LIMIT = 160 * 1024;
 
@@ -297,43 +304,46 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
   // row scale of the fused RMSNorm, r[m] = 1 / sqrt(mean(x^2) + eps): wave w reduces rows
   // w, w + 4, ... over the producer's per-tile sums of squares, lane l taking tiles
   // l, l + 64, ... (fixed order)
+  // Every load of this section is issued unconditionally through a range-checked buffer (a
+  // masked-off element reads offset NOWHERE, i.e. zero): no branch around a load, so the
+  // activations and the first weights are in flight within a few hundred cycles of the
+  // block's start.
   constexpr int RW = MT * 4;         // rows per wave, at most
   constexpr int SL = 4;              // producer tiles per lane, at most (ss_nt <= 256)
+  const bool has_norm = a.norm_w != nullptr;
+  const __amdgpu_buffer_rsrc_t rss = buf_rsrc(a.ss_in, has_norm ? Mr * a.ss_ld * 4 : 0);
   float ssv[RW][SL];
-  if (a.norm_w) {
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
+  for (int r = 0; r < RW; ++r)
 #pragma unroll
-      for (int q = 0; q < SL; ++q) {
-        const int m = wave + GEMV_WAVES * r, tt = lane + 64 * q;
-        ssv[r][q] = (m < Mr && tt < a.ss_nt) ? a.ss_in[(size_t)m * a.ss_ld + tt] : 0.f;
-      }
-  }
+    for (int q = 0; q < SL; ++q) {
+      const int m = wave + GEMV_WAVES * r, tt = lane + 64 * q;
+      const unsigned off = (has_norm && m < Mr && tt < a.ss_nt) ? (unsigned)((m * a.ss_ld + tt) * 4) : NOWHERE;
+      ssv[r][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rss, off, 0, 0));
+    }
   constexpr int XCH = 8;             // 16-byte X chunks per thread per pass
   const int cpr = ngp * 16;          // chunks per row in this K-range
   u32x4 nw[2];                       // norm weights of the K-range (cpr <= 320 chunks)
-  if (a.norm_w) {
+  const __amdgpu_buffer_rsrc_t rnw = buf_rsrc(a.norm_w, has_norm ? a.K * 2 : 0);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int k = k0 + (tid + 256 * q) * 8;
-      nw[q] = (u32x4){0u, 0u, 0u, 0u};
-      if (tid + 256 * q < cpr && k < a.K) nw[q] = *reinterpret_cast<const u32x4*>(a.norm_w + k);
-    }
+  for (int q = 0; q < 2; ++q) {
+    const int k = k0 + (tid + 256 * q) * 8;
+    const unsigned off = (has_norm && tid + 256 * q < cpr && k < a.K) ? (unsigned)(k * 2) : NOWHERE;
+    nw[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rnw, off, 0, 0));
   }
   const int xtotal = Mr * cpr;
   // chunk i of the K-range's activations is row i / cpr, chunk i % cpr: the quotient by a
   // multiply-high with ceil(2^32 / cpr), exact for i * cpr < 2^32 (i < 16 MT cpr <= 20480)
   const unsigned cpr_magic = 0xFFFFFFFFu / (unsigned)cpr + 1u;
   auto row_of = [&](int i) { return (int)__umulhi((unsigned)i, cpr_magic); };
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, Mr * a.ldx * 2);
   u32x4 xv[XCH];
 #pragma unroll
   for (int q = 0; q < XCH; ++q) {
     const int i = tid + 256 * q;
-    xv[q] = (u32x4){0u, 0u, 0u, 0u};
-    if (i < xtotal) {
-      const int m = row_of(i), ch = i - m * cpr;
-      if (k0 + ch * 8 < a.K) xv[q] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.ldx + k0 + ch * 8);
-    }
+    const int m = row_of(i), ch = i - m * cpr;
+    const unsigned off = (i < xtotal && k0 + ch * 8 < a.K) ? (unsigned)((m * a.ldx + k0 + ch * 8) * 2) : NOWHERE;
+    xv[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
   }
 
   // ---- 2. the first unit's weights ----
@@ -343,7 +353,7 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
 
   // ---- 3. row scales and norm weights, then X (normalised) into LDS while the weights are
   // in flight ----
-  if (a.norm_w) {
+  if (has_norm) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       if (tid + 256 * q < cpr) *reinterpret_cast<u32x4*>(wl + (tid + 256 * q) * 8) = nw[q];
@@ -939,9 +949,7 @@ static int occupancy(size_t lds) {
 }
 
 template <int MT, int D, int U>
-static void launch_mdu(const GemvArgs& a, size_t lds, hipStream_t st) {
-  const int nunits = a.NT * a.ksplit;
-  int G = (nunits + U - 1) / U;
+static void launch_mdu(const GemvArgs& a, size_t lds, int G, hipStream_t st) {
   G += (a.ksplit - G % a.ksplit) % a.ksplit;  // a block's K-range stays fixed: G % ksplit == 0
   hipLaunchKernelGGL((qgemv_kernel<MT, D, U>), dim3(G), dim3(256), lds, st, a);
 }
@@ -950,14 +958,18 @@ static void launch_mdu(const GemvArgs& a, size_t lds, hipStream_t st) {
 // block stages its activations once, so fewer, longer-lived blocks amortise that), but at
 // most 4: a block keeps only the next unit in flight, so longer queues (the vocab head
 // at 8 or 16 units per block) leave the weight stream latency-bound (head 110 -> 75 us).
+// With U units per block the grid is a whole number of blocks per CU, the fewest that hold
+// the units (G = CUs x ceil(units / (CUs U))): the units of one CU's blocks then differ by
+// one at most, where ceil(units / U) blocks leave some CUs a block (U units) more than others.
 template <int MT, int D>
 static void launch_md(const GemvArgs& a, size_t lds, hipStream_t st) {
   const int nunits = a.NT * a.ksplit;
   const int cap = g_cus * occupancy<MT, D, 1>(lds);
   const int need = (nunits + cap - 1) / cap;
-  if (need <= 1) launch_mdu<MT, D, 1>(a, lds, st);
-  else if (need == 2) launch_mdu<MT, D, 2>(a, lds, st);
-  else launch_mdu<MT, D, 4>(a, lds, st);
+  auto grid = [&](int U) { return std::min(nunits, g_cus * ((nunits + g_cus * U - 1) / (g_cus * U))); };
+  if (need <= 1) launch_mdu<MT, D, 1>(a, lds, nunits, st);
+  else if (need == 2) launch_mdu<MT, D, 2>(a, lds, grid(2), st);
+  else launch_mdu<MT, D, 4>(a, lds, grid(4), st);
 }
 
 template <int MT>

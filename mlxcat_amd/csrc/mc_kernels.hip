@@ -293,16 +293,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
   const int G = nq / nkv;
   const int r = blockIdx.x / nkv, kh = blockIdx.x % nkv;
   const int split = blockIdx.y;
-  const int nv = sv.n_valid[r];
-  const int nqry = nv * G;
-  if (nqry == 0) return;
-  const int base = sv.qbase[r];
-  const int kend = base + nv;
-  const int s0 = split * S * ATTN_CHUNK;
-  if (s0 >= kend) return;
-  const int s1 = min(kend, s0 + S * ATTN_CHUNK);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane >> 4, r16 = lane & 15;
-  const int slot0 = sv.row_slot0[r];
   const size_t head = (size_t)r * nkv + kh;
   const uint16_t* kbase = kv.k + head * kv.cap * D;   // [pos][d]
   const uint16_t* vbase = kv.v + head * D * kv.cap;   // [d][pos]
@@ -324,14 +315,22 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
       for (int kb = 0; kb < 4; ++kb)
         va[db][kb] = *reinterpret_cast<const s16x4_t*>(vbase + (size_t)(16 * db + r16) * kv.cap + sc + 16 * kb + 4 * c);
   };
+  const int s0 = split * S * ATTN_CHUNK;
   const int sc_first = s0 + ATTN_CHUNK * wave;
+  // the row's state, the three loads together (no branch between them)
+  const int nv = sv.n_valid[r];
+  const int base = sv.qbase[r];
+  const int slot0 = sv.row_slot0[r];
+  const int nqry = nv * G;
+  if (nqry == 0) return;
+  const int kend = base + nv;
+  if (s0 >= kend) return;
+  const int s1 = min(kend, s0 + S * ATTN_CHUNK);
   bool pre = false;  // this wave's first sub-chunk is already in registers
   if constexpr (FUSE) {
-    // loads of the prologue first (the queries of this wave, the new keys / values), then the
-    // first sub-chunk of cached keys when it holds no key of this step: the normalisation and
-    // rotation below wait only for the former (loads retire in order)
+    // the queries of this wave and the new keys / values in this block's key range
     const size_t ldq = (size_t)(nq + 2 * nkv) * D;  // row stride of the qkv projections
-    constexpr int HD = D / 2, QB = FUSE_QMAX / 4, KB = 4;
+    constexpr int HD = D / 2, QB = TP * 4, KB = 4;  // queries per wave: at most TP x 16 / 4
     const uint16_t* hq[QB];
     int pq[QB];
     bool oq[QB];
@@ -367,6 +366,8 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
 #pragma unroll
         for (int e = 0; e < D / 64; ++e) vv[i][e] = ok[i] ? hk[i][(size_t)nkv * D + lane + 64 * e] : (uint16_t)0;
     }
+    // loads of the prologue first (the queries of this wave, the new keys / values), then the
+    // first sub-chunk of cached keys when it holds no key of this step
     pre = sc_first < s1 && sc_first + ATTN_CHUNK <= base;
     if (pre) load_kv(sc_first);
     uint16_t o1[QB], o2[QB];

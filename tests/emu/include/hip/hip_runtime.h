@@ -134,6 +134,7 @@ void mfma_16x16x16_bf16(const void* a, const void* b, const float* c, float* d);
 void dma(__amdgpu_buffer_rsrc_t r, void* lds, unsigned size, unsigned off);
 emu_u32x4 bload16(__amdgpu_buffer_rsrc_t r, unsigned off);
 emu_u32x2 bload8(__amdgpu_buffer_rsrc_t r, unsigned off);
+unsigned bload4(__amdgpu_buffer_rsrc_t r, unsigned off);
 void bstore8(emu_u32x2 v, __amdgpu_buffer_rsrc_t r, unsigned off);
 void bstore16(emu_u32x4 v, __amdgpu_buffer_rsrc_t r, unsigned off);
 unsigned char* block_lds();
@@ -223,10 +224,12 @@ using std::min;
 // variadic: the stored value may be a compound literal with commas
 inline emu_u32x4 emu_bl16(__amdgpu_buffer_rsrc_t r, unsigned off, int, int) { return emu::bload16(r, off); }
 inline emu_u32x2 emu_bl8(__amdgpu_buffer_rsrc_t r, unsigned off, int, int) { return emu::bload8(r, off); }
+inline unsigned emu_bl4(__amdgpu_buffer_rsrc_t r, unsigned off, int, int) { return emu::bload4(r, off); }
 inline void emu_bs8(emu_u32x2 v, __amdgpu_buffer_rsrc_t r, unsigned off, int, int) { emu::bstore8(v, r, off); }
 inline void emu_bs16(emu_u32x4 v, __amdgpu_buffer_rsrc_t r, unsigned off, int, int) { emu::bstore16(v, r, off); }
 #define __builtin_amdgcn_raw_buffer_load_b128(...) emu_bl16(__VA_ARGS__)
 #define __builtin_amdgcn_raw_buffer_load_b64(...) emu_bl8(__VA_ARGS__)
+#define __builtin_amdgcn_raw_buffer_load_b32(...) emu_bl4(__VA_ARGS__)
 #define __builtin_amdgcn_raw_buffer_store_b64(...) emu_bs8(__VA_ARGS__)
 #define __builtin_amdgcn_raw_buffer_store_b128(...) emu_bs16(__VA_ARGS__)
 
