@@ -177,6 +177,16 @@ int mc_batch_trim(mc_batch* b, int32_t n);
 /* Per-row ragged rollback (no reference counterpart: the reference drops the forked
  * cache wholesale).  Drops min(n, len) trailing positions of one row. */
 int mc_batch_rollback(mc_batch* b, int32_t row, int32_t n);
+/* BatchKVCache.filter(keeping:) (BatchCache.swift:217-246): rows[0..n) of the batch, in that
+ * order, become rows 0..n-1 with their K/V, lengths, token histories and sampler state
+ * (a row may be listed more than once, as the reference's take() allows); the remaining
+ * rows are left empty (inactive, no K/V).  Rows have no left padding to drop. */
+int mc_batch_filter(mc_batch* b, const int32_t* rows, int32_t n);
+/* BatchKVCache.extract(_:) (BatchCache.swift:196-215): one row's K/V, positions
+ * [0, kv_len), copied into row dst_row of dst (a batch of a model with the same K/V shape,
+ * on the same device, or the same batch); that row becomes inactive with this K/V and
+ * length, ready for mc_batch_insert_prefilled.  MC_E_CAPACITY if the K/V does not fit. */
+int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int32_t dst_row);
 int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len);
 /* Copy one row's K (which_v = 0) or V (1) of one layer to host: [n_kv][len][d] bf16. */
 int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t which_v, uint16_t* out);

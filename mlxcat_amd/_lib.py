@@ -27,7 +27,7 @@ EXPORTS = [
     "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
     "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_read_attention",
     "mc_batch_read_logits",
-    "mc_batch_history",
+    "mc_batch_history", "mc_batch_filter", "mc_batch_extract_kv",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
     "mc_batch_set_profiling", "mc_batch_profile",
 ]
@@ -101,6 +101,8 @@ def load(path: str = LIB_PATH):
         "mc_batch_remove": (C.c_int, [P, I32]),
         "mc_batch_trim": (C.c_int, [P, I32]),
         "mc_batch_rollback": (C.c_int, [P, I32, I32]),
+        "mc_batch_filter": (C.c_int, [P, P, I32]),
+        "mc_batch_extract_kv": (C.c_int, [P, I32, P, I32]),
         "mc_batch_kv_len": (C.c_int, [P, I32, P]),
         "mc_batch_read_kv": (C.c_int, [P, I32, I32, I32, P]),
         "mc_batch_history": (C.c_int, [P, I32, P, I32, P]),
@@ -273,6 +275,15 @@ class Batch:
 
     def rollback(self, row: int, n: int) -> None:
         _check(load().mc_batch_rollback(self.h, row, n))
+
+    def filter(self, rows) -> None:
+        """Keep rows[i] as row i (BatchKVCache.filter(keeping:)); the other rows become empty."""
+        r = _i32(rows)
+        _check(load().mc_batch_filter(self.h, _p(r) if len(r) else None, len(r)))
+
+    def extract_kv(self, row: int, dst: "Batch", dst_row: int) -> None:
+        """Copy this row's K/V into dst's row dst_row (BatchKVCache.extract)."""
+        _check(load().mc_batch_extract_kv(self.h, row, dst.h, dst_row))
 
     def kv_len(self, row: int) -> int:
         v = C.c_int32()

@@ -439,6 +439,11 @@ struct mc_batch {
   unsigned* attn_cnt = nullptr;  // [R * n_kv] split arrivals of the fused attention, zero at rest
   StepState s;
   void* scratch = nullptr;  // one allocation for the small StepState arrays
+  size_t scratch_words = 0;
+  // the per-row arrays inside `scratch` that a row's state consists of (mc_batch_filter
+  // moves them with the row): offset and width in 32-bit words, value of an empty row
+  struct RowArr { size_t off; int w; int32_t empty; };
+  std::vector<RowArr> row_arrs;
   // pinned staging
   int32_t* h_i32 = nullptr;  // general staging
   size_t h_i32_n = 0;
@@ -622,6 +627,14 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
   uint32_t* base;
   if ((rc = dev_zero(&base, words))) { batch_free(b); return rc; }
   b->scratch = base;
+  b->scratch_words = words;
+  for (auto [o, w] : {std::pair<size_t, int>{o_active, 1}, {o_hist, b->hcap}, {o_hlen, 1}, {o_gen, 1}, {o_max, 1},
+                      {o_cur, 1}, {o_temp, 1}, {o_topp, 1}, {o_invt, 1}, {o_hseed, 1}, {o_seed, 2}, {o_ctr, 2},
+                      {o_eos, 8}, {o_neos, 1}, {o_topk, 1}, {o_mpl, 1}, {o_rp, 1}, {o_pp, 1}, {o_fp, 1},
+                      {o_mint, 1}, {o_nb, 1}, {o_bt, 16}, {o_bv, 16}, {o_proc, 1}, {o_kv, 1}})
+    b->row_arrs.push_back({o, w, 0});
+  b->row_arrs.push_back({o_rej, 1, -1});
+  b->row_arrs.push_back({o_forced, 1, -1});
   auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(base + o); };
   s.active = I32(o_active); s.hist = I32(o_hist); s.hist_len = I32(o_hlen); s.gen = I32(o_gen); s.max_gen = I32(o_max);
   s.cur = I32(o_cur); s.kv_len = I32(o_kv); s.temp = reinterpret_cast<float*>(base + o_temp);
@@ -1160,6 +1173,162 @@ extern "C" int mc_batch_trim(mc_batch* b, int32_t n) {
   for (auto& v : b->kv_len_host) v -= std::min(trimmed, v);  // per-row: min(trimmed, row length)
   if ((rc = upload_i32(b, b->s.kv_len, b->kv_len_host.data(), (size_t)b->R))) return rc;
   return trimmed;
+}
+
+// The copies that make row i hold what row rows[i] held, for i < n (a row may be listed more
+// than once): (dst, src) pairs in execution order, where -1 names one spare row.  A copy runs
+// once no pending copy still reads its destination; when only cycles remain, one destination
+// is parked in the spare first (each row is written at most once, so the copies form trees
+// and at most one cycle per connected part, and the spare is free again before the next
+// cycle needs it).
+static std::vector<std::pair<int, int>> plan_row_moves(const int32_t* rows, int n, int R) {
+  std::vector<int> src((size_t)n), readers((size_t)R, 0);
+  std::vector<char> pending((size_t)n, 0);
+  int left = 0;
+  for (int i = 0; i < n; ++i) {
+    src[(size_t)i] = rows[i];
+    if (rows[i] != i) { pending[(size_t)i] = 1; readers[(size_t)rows[i]]++; ++left; }
+  }
+  std::vector<std::pair<int, int>> out;
+  while (left > 0) {
+    bool moved = false;
+    for (int i = 0; i < n; ++i)
+      if (pending[(size_t)i] && readers[(size_t)i] == 0) {
+        out.push_back({i, src[(size_t)i]});
+        if (src[(size_t)i] >= 0) readers[(size_t)src[(size_t)i]]--;
+        pending[(size_t)i] = 0;
+        --left;
+        moved = true;
+      }
+    if (moved) continue;
+    int i = 0;  // every pending copy lies on a cycle: park one destination
+    while (!pending[(size_t)i]) ++i;
+    out.push_back({-1, i});
+    for (int j = 0; j < n; ++j)
+      if (pending[(size_t)j] && src[(size_t)j] == i) src[(size_t)j] = -1;
+    readers[(size_t)i] = 0;
+  }
+  return out;
+}
+
+// K/V positions [0, len) of one layer from (sk, sv) to (dk, dv): K blocks [n_kv][cap][d],
+// V blocks [n_kv][d][cap] with each side's own position stride.
+static int copy_kv_block(uint16_t* dk, uint16_t* dv, int dcap, const uint16_t* sk, const uint16_t* sv, int scap,
+                         int len, int nkv, int d, hipStream_t st) {
+  if (len <= 0) return MC_OK;
+  MC_HIP(hipMemcpy2DAsync(dk, (size_t)dcap * d * 2, sk, (size_t)scap * d * 2, (size_t)len * d * 2, (size_t)nkv,
+                          hipMemcpyDeviceToDevice, st));
+  MC_HIP(hipMemcpy2DAsync(dv, (size_t)dcap * 2, sv, (size_t)scap * 2, (size_t)len * 2, (size_t)nkv * d,
+                          hipMemcpyDeviceToDevice, st));
+  return MC_OK;
+}
+
+// BatchCache.swift:217-246 filter(keeping:): the listed rows, in the order given (a row may be
+// listed twice, as take() allows), become rows 0 .. n-1 with their K/V, lengths, token
+// histories and sampler state; the other rows are left empty (inactive, no K/V).  Rows here
+// have no left padding to drop.
+extern "C" int mc_batch_filter(mc_batch* b, const int32_t* rows, int32_t n) {
+  if (!b || (n > 0 && !rows)) return fail(MC_E_INVALID, "filter: null argument");
+  if (n < 0 || n > b->R) return fail(MC_E_INVALID, "filter: row count out of range");
+  for (int i = 0; i < n; ++i)
+    if (rows[i] < 0 || rows[i] >= b->R) return fail(MC_E_INVALID, "filter: row out of range");
+  MC_HIP(hipSetDevice(b->m->device));
+  int rc = sync_kv_len(b);
+  if (rc) return rc;
+  const int R = b->R;
+  const auto& c = b->m->cfg;
+  const int nkv = c.n_kv_heads, d = c.head_dim, V = b->s.V, cap = b->cap;
+  const size_t kv_row = (size_t)nkv * cap * d;  // elements of one row's K (and of its V) in one layer
+  const bool kv = !b->m->fake;
+  // K/V and generated-token counts: row blocks moved in place, through one spare block
+  const auto plan = plan_row_moves(rows, n, R);
+  uint16_t* spare = nullptr;
+  int32_t* spare_cnt = nullptr;
+  if (std::any_of(plan.begin(), plan.end(), [](const std::pair<int, int>& p) { return p.first < 0; })) {
+    if ((kv && hipMalloc((void**)&spare, 2 * kv_row * 2) != hipSuccess) ||
+        hipMalloc((void**)&spare_cnt, (size_t)V * 4) != hipSuccess) {
+      if (spare) (void)hipFree(spare);
+      return fail(MC_E_NOMEM, "filter: no device memory for the spare row");
+    }
+  }
+  // the per-row state arrays (lengths included)
+  std::vector<uint32_t> h(b->scratch_words), o;
+  if (hipMemcpy(h.data(), b->scratch, h.size() * 4, hipMemcpyDeviceToHost) == hipSuccess) {
+    o = h;
+    for (const auto& a : b->row_arrs)
+      for (int i = 0; i < R; ++i)
+        for (int e = 0; e < a.w; ++e)
+          o[a.off + (size_t)i * a.w + e] = i < n ? h[a.off + (size_t)rows[i] * a.w + e] : (uint32_t)a.empty;
+    if (hipMemcpy(b->scratch, o.data(), o.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      rc = fail(MC_E_HIP, "filter: state upload failed");
+  } else {
+    rc = fail(MC_E_HIP, "filter: state download failed");
+  }
+  // positions each copy moves (the source's length at that point of the plan)
+  std::vector<int> lens(b->kv_len_host), move_len;
+  int spare_len = 0;
+  for (const auto& [dst, src] : plan) {
+    const int len = src < 0 ? spare_len : lens[(size_t)src];
+    move_len.push_back(len);
+    if (dst < 0) spare_len = len; else lens[(size_t)dst] = len;
+  }
+  // layer by layer, the whole plan through a one-layer spare; then the counts
+  for (int l = 0; kv && !rc && l < c.n_layers; ++l) {
+    const KVLayer& L = b->kv[(size_t)l];
+    for (size_t i = 0; i < plan.size() && !rc; ++i) {
+      const auto [dst, src] = plan[i];
+      uint16_t* dk = dst < 0 ? spare : L.k + (size_t)dst * kv_row;
+      uint16_t* dv = dst < 0 ? spare + kv_row : L.v + (size_t)dst * kv_row;
+      const uint16_t* sk = src < 0 ? spare : L.k + (size_t)src * kv_row;
+      const uint16_t* sv = src < 0 ? spare + kv_row : L.v + (size_t)src * kv_row;
+      rc = copy_kv_block(dk, dv, cap, sk, sv, cap, move_len[i], nkv, d, b->st);
+    }
+  }
+  for (size_t i = 0; i < plan.size() && !rc; ++i) {
+    const auto [dst, src] = plan[i];
+    int32_t* dc = dst < 0 ? spare_cnt : b->gen_cnt + (size_t)dst * V;
+    const int32_t* sc = src < 0 ? spare_cnt : b->gen_cnt + (size_t)src * V;
+    if (hipMemcpyAsync(dc, sc, (size_t)V * 4, hipMemcpyDeviceToDevice, b->st) != hipSuccess)
+      rc = fail(MC_E_HIP, "filter: copy failed");
+  }
+  const hipError_t e = hipStreamSynchronize(b->st);
+  if (spare) (void)hipFree(spare);
+  if (spare_cnt) (void)hipFree(spare_cnt);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(MC_E_HIP, "filter: copy failed");
+  return sync_kv_len(b);  // the lengths moved with the state arrays
+}
+
+// BatchCache.swift:196-215 extract(_:): one row's K/V (positions [0, kv_len)) copied into row
+// dst_row of dst, a batch of the same model; that row becomes inactive with this K/V and
+// length, ready for mc_batch_insert_prefilled.
+extern "C" int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int32_t dst_row) {
+  if (!b || !dst) return fail(MC_E_INVALID, "extract_kv: null batch");
+  int rc = check_row(b, row);
+  if (rc || (rc = check_row(dst, dst_row))) return rc;
+  const auto &c = b->m->cfg, &dc = dst->m->cfg;
+  if (b->m->device != dst->m->device || c.n_layers != dc.n_layers || c.n_kv_heads != dc.n_kv_heads ||
+      c.head_dim != dc.head_dim || b->m->fake != dst->m->fake)
+    return fail(MC_E_INVALID, "extract_kv: the batches' models differ in K/V shape or device");
+  if (b == dst && row == dst_row) return MC_OK;
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(dst)) || (rc = sync_kv_len(b))) return rc;
+  const int len = b->kv_len_host[(size_t)row];
+  if (len > dst->cap) return fail(MC_E_CAPACITY, "extract_kv: the row's K/V exceeds the destination's capacity");
+  if ((rc = set_row_i32(dst, dst->s.active, dst_row, 0))) return rc;
+  if (!b->m->fake) {
+    const size_t skv = (size_t)c.n_kv_heads * b->cap * c.head_dim, dkv = (size_t)c.n_kv_heads * dst->cap * c.head_dim;
+    for (int l = 0; l < c.n_layers; ++l) {
+      const KVLayer &S = b->kv[(size_t)l], &D = dst->kv[(size_t)l];
+      if ((rc = copy_kv_block(D.k + (size_t)dst_row * dkv, D.v + (size_t)dst_row * dkv, dst->cap,
+                              S.k + (size_t)row * skv, S.v + (size_t)row * skv, b->cap, len, c.n_kv_heads,
+                              c.head_dim, b->st)))
+        return rc;
+    }
+    MC_HIP(hipStreamSynchronize(b->st));
+  }
+  dst->kv_len_host[(size_t)dst_row] = len;
+  return set_row_i32(dst, dst->s.kv_len, dst_row, len);
 }
 
 extern "C" int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len) {

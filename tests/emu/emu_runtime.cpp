@@ -511,6 +511,10 @@ hipError_t hipMemcpy2D(void* d, size_t dp, const void* s, size_t sp, size_t w, s
   for (size_t r = 0; r < h; ++r) memmove((char*)d + r * dp, (const char*)s + r * sp, w);
   return hipSuccess;
 }
+hipError_t hipMemcpy2DAsync(void* d, size_t dp, const void* s, size_t sp, size_t w, size_t h, hipMemcpyKind k,
+                             hipStream_t) {
+  return hipMemcpy2D(d, dp, s, sp, w, h, k);
+}
 hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
   *p = malloc(n ? n : 1);
   return hipSuccess;

@@ -12,6 +12,8 @@
 //   case 6: the case-0 model, 12 rows: one verify block of 12 x 6 = 72 tokens (the M > 64 GEMM)
 //   case 7: mc_accept with random sampler options against or_accept_row
 //   case 8: mc_accept_noalloc against mc_accept, two calls
+//   case 9: the case-4 model, 4 rows: mc_batch_filter (a 3-cycle; a repeated row) and
+//           mc_batch_extract_kv + mc_batch_insert_prefilled against an unfiltered batch
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -245,6 +247,115 @@ static int noalloc_case() {
   return g_bad ? 1 : 0;
 }
 
+// case 9: rows moved by mc_batch_filter keep producing what they produce in a batch that was
+// not filtered, and a row's K/V extracted into another batch continues the same way.
+static std::vector<int32_t> case9_prompt(int r, int V) {
+  std::vector<int32_t> p((size_t)(40 + 4 * r));
+  for (size_t i = 0; i < p.size(); ++i) p[i] = r == 2 ? (int32_t)((i * 37 + 11) % V) : 100 + r + (int32_t)(i % (5 + r));
+  return p;
+}
+static mc_sampling case9_sampling(int r) {
+  mc_sampling sp{};
+  sp.reject_token = -1;
+  if (r == 1) { sp.temperature = 0.8f; sp.has_seed = 1; sp.seed = 77; sp.presence_penalty = 0.5f; }
+  return sp;
+}
+static std::vector<std::vector<int32_t>> case9_steps(mc_batch* b, int R, int K1, int n) {
+  std::vector<std::vector<int32_t>> out((size_t)R);
+  for (int st = 0; st < n; ++st) {
+    std::vector<int32_t> ot((size_t)R * K1), cnt((size_t)R), f((size_t)R);
+    check(mc_step(b, nullptr, nullptr, ot.data(), cnt.data(), f.data()), "step");
+    for (int r = 0; r < R; ++r)
+      for (int k = 0; k < cnt[(size_t)r]; ++k) out[(size_t)r].push_back(ot[(size_t)r * K1 + k]);
+  }
+  return out;
+}
+static bool case9_same_kv(mc_batch* a, int ra, mc_batch* b, int rb, const mc_model_config& c) {
+  int32_t la = 0, lb = 0;
+  check(mc_batch_kv_len(a, ra, &la), "kv_len");
+  check(mc_batch_kv_len(b, rb, &lb), "kv_len");
+  if (la != lb) return false;
+  for (int l = 0; l < c.n_layers; ++l)
+    for (int wv = 0; wv < 2; ++wv) {
+      std::vector<uint16_t> x((size_t)c.n_kv_heads * la * c.head_dim), y(x.size());
+      check(mc_batch_read_kv(a, l, ra, wv, x.data()), "read_kv");
+      check(mc_batch_read_kv(b, l, rb, wv, y.data()), "read_kv");
+      if (x != y) return false;
+    }
+  return true;
+}
+static int filter_case(mc_model* m, const mc_model_config& c) {
+  const int R = 4, K = 4, K1 = K + 1, ctx = 256, V = c.vocab;
+  mc_spec_config spec{1, K, 3, 8, 1, 0, 0};
+  auto make = [&]() {
+    mc_batch* b = nullptr;
+    check(mc_batch_create(m, R, ctx, K, &spec, &b), "batch_create");
+    for (int r = 0; r < R; ++r) {
+      auto p = case9_prompt(r, V);
+      mc_sampling sp = case9_sampling(r);
+      int32_t first = 0, fin = 0;
+      check(mc_batch_insert(b, r, p.data(), (int32_t)p.size(), 40, &sp, &first, &fin), "insert");
+    }
+    case9_steps(b, R, K1, 2);
+    return b;
+  };
+  mc_batch* ref = make();
+  const std::vector<std::vector<int32_t>> plans{{2, 0, 1}, {1, 3, 3, 0}, {}};
+  std::vector<mc_batch*> fb;
+  for (const auto& keep : plans) {
+    mc_batch* b = make();
+    check(mc_batch_filter(b, keep.data(), (int32_t)keep.size()), "filter");
+    for (size_t i = 0; i < keep.size(); ++i)
+      if (!case9_same_kv(b, (int)i, ref, keep[i], c)) { printf("filter: row %zu K/V differs\n", i); ++g_bad; }
+    for (int i = (int)keep.size(); i < R; ++i) {
+      int32_t len = -1;
+      check(mc_batch_kv_len(b, i, &len), "kv_len");
+      if (len != 0) { printf("filter: dropped row %d keeps %d positions\n", i, len); ++g_bad; }
+    }
+    fb.push_back(b);
+  }
+  // extract row 3 of the reference batch into a one-row batch, admitted from its history
+  mc_batch* one = nullptr;
+  check(mc_batch_create(m, 1, ctx, K, &spec, &one), "batch_create");
+  check(mc_batch_extract_kv(ref, 3, one, 0), "extract_kv");
+  if (!case9_same_kv(one, 0, ref, 3, c)) { printf("extract: K/V differs\n"); ++g_bad; }
+  int32_t hl = 0;
+  check(mc_batch_history(ref, 3, nullptr, 0, &hl), "history");
+  std::vector<int32_t> hist((size_t)hl);
+  check(mc_batch_history(ref, 3, hist.data(), hl, &hl), "history");
+  mc_sampling sp3 = case9_sampling(3);
+  check(mc_batch_insert_prefilled(one, 0, hist.data(), hl, 40, &sp3), "insert_prefilled");
+  const auto want = case9_steps(ref, R, K1, 3);
+  for (size_t p = 0; p < plans.size(); ++p) {
+    const auto got = case9_steps(fb[p], R, K1, 3);
+    for (int i = 0; i < R; ++i) {
+      const bool kept = i < (int)plans[p].size();
+      const auto& w = kept ? want[(size_t)plans[p][(size_t)i]] : std::vector<int32_t>{};
+      printf("plan %zu row %d (%s): %zu tokens%s\n", p, i, kept ? "kept" : "empty", got[(size_t)i].size(),
+             got[(size_t)i] == w ? "" : "  DIFFERS");
+      if (got[(size_t)i] != w) ++g_bad;
+    }
+    mc_batch_destroy(fb[p]);
+  }
+  const auto got1 = case9_steps(one, 1, K1, 3);
+  printf("extracted row: %zu tokens (%zu in the batch)%s\n", got1[0].size(), want[3].size(),
+         got1[0] == want[3] ? "" : "  DIFFERS");
+  if (got1[0] != want[3] || want[3].empty()) ++g_bad;
+  // errors: a row out of range, a capacity too small
+  const int32_t bad[1] = {R};
+  if (mc_batch_filter(ref, bad, 1) != MC_E_INVALID) { printf("filter accepted row %d\n", R); ++g_bad; }
+  mc_batch* tiny = nullptr;
+  check(mc_batch_create(m, 1, 64, K, &spec, &tiny), "batch_create");
+  if (mc_batch_extract_kv(ref, 3, tiny, 0) != MC_E_CAPACITY) { printf("extract ignored capacity\n"); ++g_bad; }
+  mc_batch_destroy(tiny);
+  mc_batch_destroy(one);
+  mc_batch_destroy(ref);
+  printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
+  if (emu::oob_loads || emu::oob_stores) ++g_bad;
+  printf("%s\n", g_bad ? "FAIL" : "OK");
+  return g_bad ? 1 : 0;
+}
+
 int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
@@ -260,7 +371,7 @@ int main(int argc, char** argv) {
   if (cs == 3) {  // 8 kv heads, GQA group 4
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
-  if (cs == 4) {  // speculative steps: padding slots
+  if (cs == 4 || cs == 9) {  // speculative steps: padding slots
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
   if (cs == 5) {  // Qwen3-MoE: 16 experts of width 128, top-4 (a 40-token prefill gives experts > 16 pairs)
@@ -271,6 +382,7 @@ int main(int argc, char** argv) {
   mc_model* m = nullptr;
   check(mc_model_create(&c, &m), "model_create");
   check(mc_model_init_synthetic(m, SEED), "init_synthetic");
+  if (cs == 9) return filter_case(m, c);
   mc_spec_config spec{1, 5, 3, 8, 1, 0, 0};
   mc_batch* b = nullptr;
   check(mc_batch_create(m, 1, ctx, 5, &spec, &b), "batch_create");
