@@ -63,7 +63,7 @@ def step_bytes(cfg: dict, ctx_lens, M: int) -> float:
     return weights + sum(ctx_lens) * kv_tok + M * kv_tok + M * V * 2
 
 
-def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = False):
+def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = False, decode: int = DECODE):
     """The 256-token decode of the workload: W warmup steps and an untimed prefix, then the
     timed steps, placed so that the timed window ends near token 256 (the rows' budget is
     256 plus the timed steps' worth, so no row finishes inside it).  forced: exactly L drafts
@@ -78,7 +78,7 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = Fa
     m = hip.Model(QWEN3_4B)
     m.init_synthetic(SEED)
     rng = np.random.default_rng(SEED + 17)
-    max_new = DECODE + (steps + 1) * (K_DRAFT + 1)
+    max_new = decode + (steps + 1) * (K_DRAFT + 1)
     ctx = PROMPT_LEN + max_new + K_DRAFT + 16
     b = hip.Batch(m, rows, ctx, spec_cfg(rows))
     generated = np.ones(rows, dtype=np.int64)  # the first token, sampled at admission
@@ -91,7 +91,7 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = Fa
     # untimed prefix: until the timed steps at the warm-up rate end at token DECODE
     rate = max(1.0, (generated.min() - 1) / max(1, warmup))
     prefix = 0
-    while generated.min() < DECODE - steps * rate and prefix < 4 * DECODE:
+    while generated.min() < decode - steps * rate and prefix < 4 * decode:
         generated += b.step(fa())[1]
         prefix += 1
     st0 = b.stats()
@@ -246,12 +246,29 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b8", action="store_true")
+    ap.add_argument("--no-forced", action="store_true", help="skip the forced accept-length run")
+    ap.add_argument("--decode", type=int, default=DECODE,
+                    help="tokens decoded by the end of the timed window (shorter for counter runs, where every "
+                         "launch is serialised)")
     ap.add_argument("--config", choices=sorted(CONFIGS), default=None,
                     help="measure one of the other workloads instead (its own JSON line)")
     ap.add_argument("--copy-ref", action="store_true",
                     help="only copy 256 MiB three times (a plain copy kernel of known size: the scale of the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only the HBM read ceiling: a streaming read of 9 MB .. 4 GiB per launch, each launch "
+                         "from its own slice of a pool larger than the Infinity Cache")
     a = ap.parse_args()
+    if a.read_probe:
+        from mlxcat_amd import _lib as hip
+        hip.load().mc_set_device(0)
+        for nbytes, launches in ((9 << 20, 2000), (28 << 20, 1000), (64 << 20, 500), (219 << 20, 200),
+                                 (1 << 30, 50), (4 << 30, 20)):
+            us, gbs = hip.probe_hbm_read(nbytes, launches)
+            print(json.dumps({"probe": "hbm_read", "bytes_per_launch": nbytes, "launches": launches,
+                              "us_per_launch": round(us, 3), "GB_per_s": round(gbs, 1),
+                              "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+        return
     if a.copy_ref:
         import torch
         src = torch.ones(256 << 18, dtype=torch.float32, device="cuda")
@@ -273,9 +290,9 @@ def main():
         print("bench.py measures one GPU: the speculative step is built and measured on a single MI355X "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
-    b1 = run_gpu(1, a.steps, a.warmup, profile=True)
-    b1f = run_gpu(1, a.steps, a.warmup, profile=False, forced=True)
-    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False)
+    b1 = run_gpu(1, a.steps, a.warmup, profile=True, decode=a.decode)
+    b1f = None if a.no_forced else run_gpu(1, a.steps, a.warmup, profile=False, forced=True, decode=a.decode)
+    b8 = None if a.no_b8 else run_gpu(8, max(8, a.steps // 2), a.warmup, profile=False, decode=a.decode)
     cpu = None if a.no_cpu else run_cpu(1)
     cpu8 = None if (a.no_cpu or a.no_b8) else run_cpu(8, budget_s=10.0)
     if cpu is not None and cpu8 is not None:
@@ -297,7 +314,7 @@ def main():
         "data": "synthetic (random-init MLX 4-bit affine g64 weights, seeded copy-span prompts)",
         "config": {"workload": "Qwen3-4B-shape 4-bit g64 n-gram speculative step, batch 1, K=5, match 3, "
                                "2048-token prompt, greedy, 256-token decode", "batch": 1, "k_draft": K_DRAFT,
-                   "prompt": PROMPT_LEN, "decode": DECODE, "timed_tokens": b1["timed_tokens"]},
+                   "prompt": PROMPT_LEN, "decode": a.decode, "timed_tokens": b1["timed_tokens"]},
         "tokens_per_step": round(b1["tokens_per_step"], 3),
         "draft_hit_rate": round(b1["batches"] / a.steps, 3),
         "accepted_drafts_per_step": round(b1["accepted"] / a.steps, 3),
@@ -310,7 +327,7 @@ def main():
                      "kernel": g["kernel"], "launches_per_step": g["launches"],
                      "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 3),
                      "alg_bytes_per_launch": round(g["bytes"] / max(1, g["launches"]))},
-        "forced_accept": {"schedule": "exactly L ~ U[0, K] drafts accepted per step, then the history's next token "
+        "forced_accept": None if b1f is None else {"schedule": "exactly L ~ U[0, K] drafts accepted per step, then the history's next token "
                                       "(a stress of the speculative mechanics: the row keeps copying its history, "
                                       "so every step proposes; the tokens are not the model's)",
                           "tok_s": round(b1f["tok_s"], 2),

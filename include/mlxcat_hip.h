@@ -270,6 +270,15 @@ int mc_batch_call_widths(mc_batch* b, int32_t* out, int32_t cap);
 int mc_batch_set_profiling(mc_batch* b, int32_t enabled);
 int mc_batch_profile(mc_batch* b, int32_t kind, double* ms, double* bytes, int32_t* launches);
 
+/* ---- measurement ---- */
+/* No counterpart in the reference: the HBM read ceiling for the roofline fractions.  Reads
+ * `bytes` per launch, `launches` launches back to back on a new stream of the current
+ * device, each from its own slice of a pool of at least 1 GiB and 2 x bytes (larger than the
+ * 256 MB Infinity Cache, so no launch hits a cache), for grids of 1.5, 3 and 6 blocks per CU;
+ * returns the fastest grid's average time per launch (event-timed, launch gaps included)
+ * and bytes / that time.  Allocates and frees the pool. */
+int mc_probe_hbm_read(int64_t bytes, int32_t launches, double* us_per_launch, double* gb_per_s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,7 +29,7 @@ EXPORTS = [
     "mc_batch_read_logits",
     "mc_batch_history", "mc_batch_filter", "mc_batch_extract_kv",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
-    "mc_batch_set_profiling", "mc_batch_profile",
+    "mc_batch_set_profiling", "mc_batch_profile", "mc_probe_hbm_read",
 ]
 
 
@@ -102,6 +102,7 @@ def load(path: str = LIB_PATH):
         "mc_batch_trim": (C.c_int, [P, I32]),
         "mc_batch_rollback": (C.c_int, [P, I32, I32]),
         "mc_batch_filter": (C.c_int, [P, P, I32]),
+        "mc_probe_hbm_read": (C.c_int, [C.c_int64, I32, P, P]),
         "mc_batch_extract_kv": (C.c_int, [P, I32, P, I32]),
         "mc_batch_kv_len": (C.c_int, [P, I32, P]),
         "mc_batch_read_kv": (C.c_int, [P, I32, I32, I32, P]),
@@ -425,3 +426,11 @@ def accept_noalloc(logits_ptr: int, vocab: int, B: int, K: int, drafts_ptr: int,
                                     C.c_void_p(uniforms_ptr) if uniforms_ptr else None, acceptance,
                                     C.c_void_p(out_ptr), C.c_void_p(n_emit_ptr), C.c_void_p(keep_ptr),
                                     C.c_void_p(nacc_ptr)))
+
+
+def probe_hbm_read(nbytes: int, launches: int) -> tuple[float, float]:
+    """(us per launch, GB/s) of a streaming read of nbytes per launch, each launch from its
+    own slice of a pool larger than the Infinity Cache (mc_probe_hbm_read)."""
+    us, gbs = C.c_double(), C.c_double()
+    _check(load().mc_probe_hbm_read(nbytes, launches, C.byref(us), C.byref(gbs)))
+    return us.value, gbs.value

@@ -10,7 +10,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "csrc", "_obj")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libmlxcat_hip.so")
-SOURCES = ["mc_api.hip", "mc_gemv.hip", "mc_kernels.hip", "mc_step.hip"]
+SOURCES = ["mc_api.hip", "mc_gemv.hip", "mc_kernels.hip", "mc_step.hip", "mc_probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-fp32 instructions are disabled for every kernel; the host pass ignores the flag.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
