@@ -198,6 +198,10 @@ int mc_batch_read_attention(mc_batch* b, int32_t M, uint16_t* out);
 /* Logits of token slots [slot0, slot0 + n) of the last forward: out[n][vocab] bf16.  After
  * mc_step, row r's verify position j is slot r * (K + 1) + j. */
 int mc_batch_read_logits(mc_batch* b, int32_t slot0, int32_t n, uint16_t* out);
+/* Qwen3-MoE: the last layer's bf16 router logits of the last forward's token slots,
+ * out[M][n_experts], for forwards of at most 64 slots (parity inspection of the top-k
+ * routing, like mc_batch_read_attention). */
+int mc_batch_read_router(mc_batch* b, int32_t M, uint16_t* out);
 
 /* ---- forward: LanguageModel.callAsFunction(LMInput.Text, cache:, state:)
  * (BatchGenerator.swift:900-904).  counts[r] new tokens for each listed row, positions

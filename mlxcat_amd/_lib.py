@@ -27,7 +27,7 @@ EXPORTS = [
     "mc_batch_insert", "mc_batch_insert_prefilled", "mc_batch_fill_synthetic_kv", "mc_batch_remove",
     "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_read_attention",
     "mc_batch_read_logits",
-    "mc_batch_history", "mc_batch_filter", "mc_batch_extract_kv",
+    "mc_batch_history", "mc_batch_filter", "mc_batch_extract_kv", "mc_batch_read_router",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
     "mc_batch_set_profiling", "mc_batch_profile", "mc_probe_hbm_read",
 ]
@@ -109,6 +109,7 @@ def load(path: str = LIB_PATH):
         "mc_batch_history": (C.c_int, [P, I32, P, I32, P]),
         "mc_batch_read_attention": (C.c_int, [P, I32, P]),
         "mc_batch_read_logits": (C.c_int, [P, I32, I32, P]),
+        "mc_batch_read_router": (C.c_int, [P, I32, P]),
         "mc_forward": (C.c_int, [P, I32, P, P, P, P]),
         "mc_ngram_propose": (C.c_int, [P, P, I32, I32, I32, P, I32, P, P]),
         "mc_accept": (C.c_int, [P, I32, I32, P, P, I32, P, P, P, P, P, P, I32, P, P, P, P]),
@@ -309,6 +310,12 @@ class Batch:
         position j is slot r * (K + 1) + j)."""
         out = np.zeros((n, self.model.cfg.vocab), dtype=np.uint16)
         _check(load().mc_batch_read_logits(self.h, slot0, n, _p(out)))
+        return out
+
+    def read_router(self, M: int) -> np.ndarray:
+        """Qwen3-MoE: the last layer's router logits of the last forward's slots [M][E]."""
+        out = np.zeros((M, self.model.cfg.n_experts), dtype=np.uint16)
+        _check(load().mc_batch_read_router(self.h, M, _p(out)))
         return out
 
     def history(self, row: int) -> list[int]:

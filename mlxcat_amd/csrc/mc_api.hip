@@ -1382,6 +1382,17 @@ extern "C" int mc_batch_read_attention(mc_batch* b, int32_t M, uint16_t* out) {
   return MC_OK;
 }
 
+extern "C" int mc_batch_read_router(mc_batch* b, int32_t M, uint16_t* out) {
+  if (!b || !out || M < 0) return fail(MC_E_INVALID, "read_router: bad argument");
+  const auto& c = b->m->cfg;
+  if (!b->moe_logits) return fail(MC_E_STATE, "read_router: not a mixture-of-experts model");
+  if (M > b->last_M || M > 64) return fail(MC_E_STATE, "read_router: the last forward's last 64-token chunk has fewer slots");
+  MC_HIP(hipSetDevice(b->m->device));
+  MC_HIP(hipStreamSynchronize(b->st));
+  MC_HIP(hipMemcpy(out, b->moe_logits, (size_t)M * c.n_experts * 2, hipMemcpyDeviceToHost));
+  return MC_OK;
+}
+
 extern "C" int mc_batch_read_logits(mc_batch* b, int32_t slot0, int32_t n, uint16_t* out) {
   if (!b || !out || slot0 < 0 || n < 0) return fail(MC_E_INVALID, "read_logits: bad argument");
   const int V = b->m->cfg.vocab;

@@ -192,6 +192,9 @@ int or_forward_attn(or_model* m, int nrows, const int32_t* rows, const int32_t* 
                     const int32_t* tokens, uint16_t* logits, uint16_t* hidden, uint16_t* attn);
 
 void or_set_threads(int n);
+/* While out != NULL, every Qwen3-MoE forward writes each layer's bf16 router logits there,
+ * out[layer][M][n_experts] (the values the top-k selection reads); NULL to stop. */
+void or_capture_router(uint16_t* out);
 /* reversed != 0: every fp32 reduction of the forward (linears, RMSNorm, attention) runs in
  * another order (test aid: the rounding noise floor between two exact summation orders) */
 void or_set_reduction_order(int reversed);

@@ -326,6 +326,9 @@ int or_forward_trace(or_model* m, int nrows, const int32_t* rows, const int32_t*
   return or_forward_attn(m, nrows, rows, counts, tokens, logits, hidden, NULL);
 }
 
+static uint16_t* g_router_out = NULL;
+void or_capture_router(uint16_t* out) { g_router_out = out; }
+
 int or_forward_attn(or_model* m, int nrows, const int32_t* rows, const int32_t* counts,
                     const int32_t* tokens, uint16_t* logits, uint16_t* hidden, uint16_t* attn) {
   const or_config* c = &m->cfg;
@@ -454,6 +457,8 @@ int or_forward_attn(or_model* m, int nrows, const int32_t* rows, const int32_t* 
         float* r = rl + (size_t)t * E;
         float mxr = -INFINITY;
         for (int e = 0; e < E; ++e) { r[e] = bf(tobf(r[e])); if (r[e] > mxr) mxr = r[e]; }
+        if (g_router_out)
+          for (int e = 0; e < E; ++e) g_router_out[((size_t)l * M + t) * E + e] = tobf(r[e]);
         float den = 0.0f;
         for (int e = 0; e < E; ++e) { r[e] = expf(r[e] - mxr); den += r[e]; }
         for (int e = 0; e < E; ++e) r[e] /= den;

@@ -109,6 +109,7 @@ def lib():
             "or_forward_attn": (I, [P, I, P, P, P, P, P, P]),
             "or_set_threads": (None, [I]),
             "or_set_reduction_order": (None, [I]),
+            "or_capture_router": (None, [P]),
             "or_generator_create": (P, [P, P, I, I, U64]),
             "or_generator_destroy": (None, [P]),
             "or_generator_insert": (I, [P, I, P, I, I, P, P]),
@@ -268,21 +269,29 @@ class Model:
         lib().or_kv_read(self.h, layer, row, which_v, _p(out))
         return out
 
-    def forward(self, rows, counts, tokens, want_logits=True, trace=False, attention=False):
+    def forward(self, rows, counts, tokens, want_logits=True, trace=False, attention=False, router=False):
         """Logits [M][V]; with trace=True also the hidden states, with attention=True also each
-        layer's attention output [layers][M][nq * d] (returned as a tuple in that order)."""
+        layer's attention output [layers][M][nq * d], with router=True also each layer's bf16
+        router logits [layers][M][n_experts] (returned as a tuple in that order)."""
         rows, counts, tokens = i32(rows), i32(counts), i32(tokens)
         M = int(counts.sum())
         c = self.cfg
         lg = np.zeros((M, c.vocab), dtype=np.uint16) if want_logits else None
         hid = np.zeros((c.n_layers + 1, M, c.hidden), dtype=np.uint16) if trace else None
         att = np.zeros((c.n_layers, M, c.n_q_heads * c.head_dim), dtype=np.uint16) if attention else None
-        rc = lib().or_forward_attn(self.h, len(rows), _p(rows), _p(counts), _p(tokens),
-                                   _p(lg) if lg is not None else None, _p(hid) if hid is not None else None,
-                                   _p(att) if att is not None else None)
+        rl = np.zeros((c.n_layers, M, max(1, c.n_experts)), dtype=np.uint16) if router else None
+        if rl is not None:
+            lib().or_capture_router(_p(rl))
+        try:
+            rc = lib().or_forward_attn(self.h, len(rows), _p(rows), _p(counts), _p(tokens),
+                                       _p(lg) if lg is not None else None, _p(hid) if hid is not None else None,
+                                       _p(att) if att is not None else None)
+        finally:
+            if rl is not None:
+                lib().or_capture_router(None)
         if rc:
             raise RuntimeError(f"or_forward failed: {rc}")
-        out = [lg] + ([hid] if trace else []) + ([att] if attention else [])
+        out = [lg] + ([hid] if trace else []) + ([att] if attention else []) + ([rl] if router else [])
         return tuple(out) if len(out) > 1 else lg
 
 
