@@ -18,9 +18,12 @@
 //     an arrival counter per tile, so no L2 writeback/invalidate fence is needed;
 //     the last-arriving block reduces them in K-range order and runs the epilogue
 //     (store, residual add, or SwiGLU of interleaved gate/up rows).
-// The K-range plan depends only on (N, K) and the M class (M <= 16 or M <= 64), and
-// every reduction runs in a fixed order, so a token's result is bit-identical
-// whatever the number of tokens in the launch (within the class).
+// For M <= 64 the K-range plan depends only on (N, K) and the M class (M <= 16 or
+// M <= 64), and every reduction runs in a fixed order, so a token's result is
+// bit-identical whatever the number of tokens in the launch within its class.  The
+// M > 64 GEMM's split-K plan depends on M (and the CU count), and the attention's split
+// on the batch's rows and capacity, so across batch shapes results agree to rounding,
+// not bit for bit.
 #include "mc_gemv.hpp"
 
 #include <algorithm>
@@ -246,12 +249,24 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
   epilogue<MT>(a, acc, t, c, r16);
 }
 
+// Ordering of the split-K hand-over.  A K-range's partials are agent-scope (sc1) stores,
+// which gfx950 writes through to memory; the writer waits for them (s_waitcnt vmcnt(0)
+// after a workgroup release fence) before its relaxed agent-scope atomicAdd on the tile's
+// counter, so the partials are in memory when the counter moves.  The last arriver learns
+// it is last from the atomic's returned value (the wave waits for it before the branch),
+// and only then loads the partials, again with agent-scope (sc1) loads, which read memory
+// rather than a possibly stale L2 line, so no cache invalidation is needed on that path.
+// What the relaxed atomics alone do not promise is the compiler's order: the memory
+// clobber after the branch keeps the partial loads below the atomic.  (An agent-scope
+// acquire fence there would say the same in the memory model's terms, but it also emits an
+// L2 invalidate per finished tile, measured at +6% on the batch-1 verify step.)
 template <int MT>
 __device__ inline void arrive(const GemvArgs& a, int t, int lane, int c, int r16) {
   unsigned arrived = 0u;
   if (lane == 0) arrived = atomicAdd(a.counters + t, 1u);
   arrived = __shfl(arrived, 0);
   if (arrived != (unsigned)(a.ksplit - 1)) return;
+  MC_FENCE();
   finish_tile<MT>(a, t, lane, c, r16);
 }
 
@@ -265,6 +280,7 @@ __device__ inline void arrive_units(const GemvArgs& a, int t0, int ts, int lane,
     unsigned arrived = 0u;
     if (t < a.NT) arrived = atomicAdd(a.counters + t, 1u);
     unsigned long long last = __ballot(t < a.NT && arrived == (unsigned)(a.ksplit - 1));
+    MC_FENCE();  // the partial loads stay below the atomics, as in arrive()
     while (last) {
       const int i = __ffsll((long long)last) - 1;
       last &= last - 1;

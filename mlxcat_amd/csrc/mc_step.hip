@@ -583,7 +583,9 @@ __device__ int decide_row(const StepState& s, int r, int32_t* out, int* keep, in
       }
       if (!all) {
         *rejected = 1;                                          // :938
-        out[0] = st[0];                                         // :939 one-token decode == position 0
+        out[0] = st[0];                                         // :939 the one-token decode: position 0
+        // (bit-identical to a separate one-token forward within the M <= 16 class at the same
+        // batch shape; across classes it agrees to rounding)
         n = 1;
       } else {
         n = na;
