@@ -111,7 +111,8 @@ def run_gpu(rows: int, steps: int, warmup: int, profile: bool, forced: bool = Fa
                timed_tokens=[int(generated.min() - emitted // rows), int(generated.max())], prefix_steps=prefix)
     out["step_hbm_gbs"] = out["bytes_per_step"] / (out["ms_per_step"] * 1e-3) / 1e9
     if profile:
-        # kind 0: the dequant GEMVs of the verify forward, timed with HIP events on the batch stream
+        # kind 0: the dequant GEMVs of the verify forward, each timed by the start and end events
+        # of its own launch (hipExtLaunchKernel on the batch stream: the kernel's execution)
         b.set_profiling(True)
         acc = [0.0, 0.0, 0]
         for _ in range(3):

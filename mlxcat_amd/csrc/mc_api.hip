@@ -687,6 +687,22 @@ static int prof_end(mc_batch* b, size_t e0, int kind, double bytes) {
   b->recs.push_back({kind, e0, e1, bytes});
   return MC_OK;
 }
+// One GEMV / GEMM kernel timed by its own launch (start and end of its execution, not the
+// dispatch gap before it): the next such launch on this thread records into two events.
+static int prof_kernel(mc_batch* b, int kind, double bytes) {
+  if (!b->profiling) return MC_OK;
+  if (b->ev_used + 2 > b->ev.size()) {
+    for (int i = 0; i < 64; ++i) {
+      hipEvent_t e;
+      MC_HIP(hipEventCreate(&e));
+      b->ev.push_back(e);
+    }
+  }
+  const size_t e0 = b->ev_used++, e1 = b->ev_used++;
+  gemv_time_next_launch(b->ev[e0], b->ev[e1]);
+  b->recs.push_back({kind, e0, e1, bytes});
+  return MC_OK;
+}
 
 // Algorithmic HBM bytes of one forward over M slots: every linear's packed weights
 // (0.5625 B per weight), the cached K/V read, the new K/V written, the bf16 logits.
@@ -731,10 +747,10 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
     a.amax = amax;
     a.part = b->gemv_part; a.part_floats = b->gemv_part_n;
     a.counters = b->gemv_cnt; a.counters_n = b->gemv_cnt_n;
-    size_t e0 = 0;
-    if ((rc = prof_begin(b, &e0))) return rc;
-    if ((rc = qgemm_launch(a, b->st))) return rc;
-    return prof_end(b, e0, 0, L.alg_bytes());
+    if ((rc = prof_kernel(b, 0, L.alg_bytes()))) return rc;
+    rc = qgemm_launch(a, b->st);
+    gemv_time_next_launch(nullptr, nullptr);  // consumed by the launch, or dropped on an error
+    return rc;
   }
   for (int m0 = 0; m0 < M; m0 += 64) {
     const int mc = std::min(64, M - m0);
@@ -755,11 +771,11 @@ static int run_gemv(mc_batch* b, const QLinear& L, const uint16_t* x, int ldx, c
     a.part = b->gemv_part; a.part_floats = b->gemv_part_n;
     a.counters = b->gemv_cnt; a.counters_n = b->gemv_cnt_n; a.epi = epi;
     if (amax) a.amax = amax + (size_t)m0 * L.NT;
-    size_t e0 = 0;
-    int rc = prof_begin(b, &e0);
+    int rc = prof_kernel(b, 0, L.alg_bytes());
     if (rc) return rc;
-    if ((rc = gemv_launch(a, MT, b->st))) return rc;
-    if ((rc = prof_end(b, e0, 0, L.alg_bytes()))) return rc;
+    rc = gemv_launch(a, MT, b->st);
+    gemv_time_next_launch(nullptr, nullptr);
+    if (rc) return rc;
   }
   return MC_OK;
 }

@@ -26,6 +26,10 @@
 // not bit for bit.
 #include "mc_gemv.hpp"
 
+#ifndef MC_EMULATE
+#include <hip/hip_ext.h>
+#endif
+
 #include <algorithm>
 
 namespace mc {
@@ -846,6 +850,23 @@ __global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
     if (tw + n < a.NT) arrive<QG_MB>(e, tw + n, lane, c, r16);
 }
 
+static thread_local hipEvent_t t_launch_ev[2] = {nullptr, nullptr};
+void gemv_time_next_launch(hipEvent_t start, hipEvent_t stop) {
+  t_launch_ev[0] = start;
+  t_launch_ev[1] = stop;
+}
+
+// hipLaunchKernelGGL, or hipExtLaunchKernelGGL with the events of gemv_time_next_launch
+template <typename F, typename... Args>
+static void launch_gemv_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+  if (t_launch_ev[0]) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, st, t_launch_ev[0], t_launch_ev[1], 0u, args...);
+    t_launch_ev[0] = t_launch_ev[1] = nullptr;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+  }
+}
+
 static int device_cus();
 
 // Split-K plan of the large-M GEMM: the K-range length (group pairs) and the number of
@@ -900,7 +921,7 @@ int qgemm_launch(const GemvArgs& a, hipStream_t st) {
                        (size_t)a.counters_n < (size_t)mblocks * a.NT))
     return fail(MC_E_INVALID, "qgemm: split-K workspace too small");
   const dim3 grid((unsigned)((a.NT + 4 * QG_NTW - 1) / (4 * QG_NTW)), mblocks, (unsigned)p.ksplit);
-  hipLaunchKernelGGL(qgemm_kernel, grid, dim3(256), qgemm_lds_bytes(), st, p);
+  launch_gemv_kernel(qgemm_kernel, grid, dim3(256), qgemm_lds_bytes(), st, p);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
@@ -967,7 +988,7 @@ static int occupancy(size_t lds) {
 template <int MT, int D, int U>
 static void launch_mdu(const GemvArgs& a, size_t lds, int G, hipStream_t st) {
   G += (a.ksplit - G % a.ksplit) % a.ksplit;  // a block's K-range stays fixed: G % ksplit == 0
-  hipLaunchKernelGGL((qgemv_kernel<MT, D, U>), dim3(G), dim3(256), lds, st, a);
+  launch_gemv_kernel(qgemv_kernel<MT, D, U>, dim3(G), dim3(256), lds, st, a);
 }
 
 // Units per block: enough that one round of resident blocks covers the launch (every
@@ -1007,7 +1028,7 @@ static void launch_mid_d(const GemvArgs& a, size_t lds, hipStream_t st) {
     occ = 1;
   const int groups = (a.NT + MID_WAVES - 1) / MID_WAVES;
   const int G1 = std::max(1, std::min(groups, device_cus() * occ / a.ksplit));
-  hipLaunchKernelGGL((qgemv_mid_kernel<MT, D>), dim3(G1 * a.ksplit), dim3(MID_THREADS), lds, st, a);
+  launch_gemv_kernel(qgemv_mid_kernel<MT, D>, dim3(G1 * a.ksplit), dim3(MID_THREADS), lds, st, a);
 }
 
 template <int MT>

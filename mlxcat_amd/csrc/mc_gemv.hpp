@@ -83,6 +83,10 @@ int gemv_launch(const GemvArgs& a, int MT, hipStream_t st);
 // M > 64 tokens: every token tile of a block against each dequantised K-step (input rows
 // already normalised: norm_w must be NULL)
 int qgemm_launch(const GemvArgs& a, hipStream_t st);
+// The next GEMV / GEMM kernel launched on this thread records its own start and end in
+// these events (hipExtLaunchKernel: the kernel's execution, without the dispatch gap
+// before it); consumed by that launch.  Profiled steps only.
+void gemv_time_next_launch(hipEvent_t start, hipEvent_t stop);
 // Its split-K plan (group pairs per K-range, K-ranges) for M tokens on `cus` CUs, and the
 // workspace every M up to Mmax needs on the current device: partial floats and counters
 // (zero when no plan splits).

@@ -114,8 +114,10 @@ def assert_close_bf16_wide(got_u16, want_u16, atol=ATOL, rtol=RTOL, frac=0.999, 
         fl = (float((fe <= 1).mean()), float(fe.max()))
         need, cap = min(frac, fl[0] - 0.001), max(2.0, 1.25 * fl[1])
     ratio = err / bound
-    assert ratio.max() <= cap, f"{what}: max err {ratio.max():.3f} x the bound (cap {cap:.3f}; reordered oracle {fl})"
     inside = float((ratio <= 1).mean())
+    print(f"[wide] {what}: inside {inside:.5f} (required {need:.5f}), worst {ratio.max():.3f} x the bound "
+          f"(cap {cap:.3f}); reordered oracle (inside, worst) {fl}")
+    assert ratio.max() <= cap, f"{what}: max err {ratio.max():.3f} x the bound (cap {cap:.3f}; reordered oracle {fl})"
     assert inside >= need, (f"{what}: only {inside:.5f} within {atol} abs + {rtol} rel (required {need:.5f}; "
                             f"reordered oracle (inside, max ratio) {fl})")
     ws = np.sort(w, axis=-1)

@@ -153,6 +153,8 @@ void launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t, A... args)
 
 #define hipLaunchKernelGGL(kernel, grid, block, lds, stream, ...) \
   emu::launch(kernel, dim3(grid), dim3(block), (size_t)(lds), stream, __VA_ARGS__)
+#define hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ev0, ev1, flags, ...) \
+  ((void)(ev0), (void)(ev1), emu::launch(kernel, dim3(grid), dim3(block), (size_t)(lds), stream, __VA_ARGS__))
 
 #define threadIdx (*emu::g_tid)
 #define blockIdx (*emu::g_bid)

@@ -99,8 +99,8 @@ def test_batch8_llama3_8b_shape_matches_oracle(hip, oracle):
 
 
 def test_m288_qwen3_8b_shape_matches_oracle(hip, oracle):
-    """32 rows x K+1 = 9 tokens (M = 288, five launches of at most 64 rows) at the Qwen3-8B
-    layer shapes."""
+    """32 rows x K+1 = 9 tokens (M = 288: the large-M GEMM, split K) at the Qwen3-8B layer
+    shapes."""
     _rows_block_vs_oracle(hip, oracle, QWEN3_8B_1L_V4K, rows=32, ctx=48, prefill=16, width=9, seed=5)
 
 
