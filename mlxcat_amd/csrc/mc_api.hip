@@ -855,8 +855,13 @@ static int forward_slots(mc_batch* b, int M, int max_q, int lg0, int lgn) {
   const int Nqkv = (nq + 2 * nkv) * d;
   SlotView sv{s.slot_tok, s.slot_row, s.slot_pos, s.row_slot0, s.n_valid, s.qbase};
   // Attention with the q/k preparation and the split merge inside (one launch per layer
-  // instead of three) whenever a row's queries of one kv head fit its query buffer.
-  const bool fuse = attn_fuse_ok(b->R, nkv, b->aw.nchunk, max_q, nq, d);
+  // instead of three) whenever a row's queries of one kv head fit its query buffer, except
+  // for many (row, kv head) pairs over short splits: every split block repeats its queries'
+  // preparation, which at 64 pairs x 512-key splits costs more than the two launches it
+  // saves (8 rows, K = 5: 5.30 ms fused against 5.03 ms per step; 8 Llama-3-8B rows: 6.50
+  // against 6.30), while 32 rows x 16K keys (4160-key splits) and a single row gain from it.
+  const int S_attn = attn_split(b->R, nkv, b->aw.nchunk, true);
+  const bool fuse = attn_fuse_ok(b->R, nkv, b->aw.nchunk, max_q, nq, d) && (b->R * nkv < 64 || S_attn >= 16);
   if ((rc = launch_embed(m->embed, s.slot_tok, M, H, b->x, b->ssq, H / 16, b->st)))
     return rc;
   for (int l = 0; l < c.n_layers; ++l) {
