@@ -30,7 +30,9 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
 }
 
 static int g_device = 0;
-constexpr int PREFILL_CHUNK = 64;
+// Prompt prefill chunk: the reference's idle-time chunk (Scheduler.swift:670-800 uses 512
+// tokens idle, 2048 busy); more than 64 tokens run the linears through the large-M GEMM.
+constexpr int PREFILL_CHUNK = 512;
 
 // State of mc_accept_noalloc: a file-scope device array, one copy per GPU, held until the
 // process ends and shared by every call on that GPU.  Host code never names it as an
