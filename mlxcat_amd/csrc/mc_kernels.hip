@@ -657,11 +657,12 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(SlotView sv, int M, int
 // 64-key sub-chunks per block: more when the grid would exceed about 1024 blocks (fewer
 // partials to merge), at least 8 from 64 (row, kv head) pairs on (two sub-chunks per wave,
 // 4x fewer partials; batch 8 at 2K keys 5.08 -> 4.89 ms per step, 8 rows at 512-4096 keys
-// 6.71 -> 6.28 ms), else 2: a decode row spreads its heads over more CUs (a block's loads
-// are one latency-bound round; at 2K keys the fused kernel's loads took 3.7 us with 2
-// sub-chunks per block and 6.1 us with 4).
+// 6.71 -> 6.28 ms), else 3: a decode row spreads its heads over more CUs, while the
+// last-arriving block's merge reads fewer partials.  Qwen3-4B shape, one row at ~2.3K keys,
+// per step with a one-token verify / with six verify tokens: 2 sub-chunks 2.33 / 2.71 ms,
+// 3: 2.33 / 2.64, 4: 2.34 / 2.63.
 int attn_split(int R, int nkv, int nchunk, bool fused) {
-  const int smin = R * nkv >= 64 ? 8 : 2;
+  const int smin = R * nkv >= 64 ? 8 : 3;
   return std::max(smin, (R * nkv * nchunk + 1023) / 1024);
 }
 

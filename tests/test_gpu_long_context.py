@@ -22,7 +22,7 @@ CHUNK = 64
 
 def attn_split(R, nkv, nchunk):
     """Sub-chunks per attention block as the library chooses them (mc_kernels.hip attn_split)."""
-    return max(8 if R * nkv >= 64 else 2, (R * nkv * nchunk + 1023) // 1024)
+    return max(8 if R * nkv >= 64 else 3, (R * nkv * nchunk + 1023) // 1024)
 
 
 def assert_attention_close(got_u16, want_u16, nq, d, what, rel=2e-2, rtol=1e-2, frac=0.999):
