@@ -682,23 +682,25 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
 // and used against every token tile of the block
 // ---------------------------------------------------------------------------------------
 // Block (n-block, m-block): 128 weight rows (wave w owns tiles 8 nb + 2 w, + 1) x 16 MB
-// tokens, accumulators resident over the whole K.  The activations go through LDS one
+// tokens, accumulators resident over the whole K; two blocks per CU (64-token blocks keep
+// the kernel within 256 registers, so one block's waits overlap the other's MFMAs).  The activations go through LDS one
 // 128-wide K-step (group pair) at a time, double-buffered: the next step's loads are in
 // flight while the current step is computed, and its group sums are formed as it is
 // written.  The input rows are already normalised (no fused RMSNorm here).  When the
 // (weight-block, token-block) grid would leave CUs idle, K is split over blockIdx.z: each
 // K-range leaves device-coherent fp32 partials and the last arrival per tile sums them in
 // K-range order and runs the epilogue (the same protocol as the 17-64-token kernel).
-constexpr int QG_MB = 6;                 // token tiles per block (96 tokens)
+constexpr int QG_MB = 4;                 // token tiles per block (64 tokens)
 constexpr int QG_NTW = 2;                // weight tiles per wave
 constexpr int QG_RD = 4;                 // K-steps of weights held in registers (prefetch distance QG_RD - 1)
 constexpr int QG_XS = 128 + 8;           // LDS row stride (bf16) of one K-step of X
 constexpr int QG_XCH = QG_MB * 16 * 16 / 256;  // 16-byte X chunks per thread per K-step
 constexpr int QG_KSPLIT_MAX = 8;
+constexpr int QG_OCC = 2;                // resident blocks per CU (the kernel's launch bounds)
 
 size_t qgemm_lds_bytes() { return (size_t)2 * 16 * QG_MB * QG_XS * 2 + (size_t)2 * 2 * 16 * QG_MB * 4; }
 
-__global__ void __launch_bounds__(256) qgemm_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(256, 2) qgemm_kernel(GemvArgs a) {
   MC_DYN_LDS(smem);
   constexpr int MR = 16 * QG_MB;
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                          // [2][MR][QG_XS]
@@ -883,7 +885,7 @@ void qgemm_plan(int NT, int GP, int M, int cus, int* kr, int* ksplit) {
     const int r = (GP + ks - 1) / ks, kse = (GP + r - 1) / r;
     if (kse != ks) continue;  // the same split as a smaller ks
     const long blocks = tiles * kse;
-    const double rounds = (double)((blocks + cus - 1) / cus);
+    const double rounds = (double)((blocks + QG_OCC * cus - 1) / (QG_OCC * cus));
     double us = rounds * (r + 1.5) * 2.2;
     if (kse > 1) us += (double)blocks * 4 * QG_NTW * 16 * 16 * QG_MB * 4 * 2 / 4e6;
     if (ks == 1 || us < best) {

@@ -23,7 +23,7 @@
 #define __device__
 #define __global__
 #define __forceinline__ inline
-#define __launch_bounds__(x)
+#define __launch_bounds__(...)
 #define __align__(x) __attribute__((aligned(x)))
 #define __shared__ static  // blocks of an ordinary kernel run one group at a time (see run_kernel)
 
