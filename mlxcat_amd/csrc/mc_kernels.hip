@@ -230,6 +230,7 @@ int launch_qk_rope_append(const uint16_t* qkv, const uint16_t* q_norm, const uin
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 // query tiles of 16 per pass over the keys: every tile of a (row, kv head) in one pass
 // (at most 4, 64 queries), so the keys and values are read once
 inline int attn_tiles(int nqry) { return std::min(4, std::max(1, (nqry + 15) / 16)); }
@@ -300,20 +301,29 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
   constexpr int NS = D / 32, NDB = D / 16;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
   // keys sc .. sc + 63 of the cache (inside the row's cap; keys >= kend are finite and masked)
+  // in four 16-key MFMA blocks.  Slot j of block kb = 2 p + h holds key
+  //   sc + 32 p + 8 (j / 4) + 4 h + j % 4,
+  // so the 4 keys a lane holds of block 2p and the 4 of block 2p + 1 are 8 consecutive
+  // positions: one 16-byte load of a V^T row serves both blocks (the sum over keys does
+  // not depend on which slot holds which key, as long as K, the mask and V agree).
   bf16x8_t ka[4][4];
   s16x4_t va[NDB][4];
+  auto key_of = [&](int kb, int j) { return 32 * (kb >> 1) + 8 * (j >> 2) + 4 * (kb & 1) + (j & 3); };
   auto load_kv = [&](int sc) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
-        ka[kb][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)(sc + 16 * kb + r16) * D + 32 * s4 + 8 * c)
+        ka[kb][s4] = s4 < NS ? *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)(sc + key_of(kb, r16)) * D + 32 * s4 + 8 * c)
                              : __builtin_bit_cast(bf16x8_t, (u4){0u, 0u, 0u, 0u});
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        va[db][kb] = *reinterpret_cast<const s16x4_t*>(vbase + (size_t)(16 * db + r16) * kv.cap + sc + 16 * kb + 4 * c);
+      for (int p = 0; p < 2; ++p) {
+        const s16x8_t v8 = *reinterpret_cast<const s16x8_t*>(vbase + (size_t)(16 * db + r16) * kv.cap + sc + 32 * p + 8 * c);
+        va[db][2 * p] = (s16x4_t){v8[0], v8[1], v8[2], v8[3]};
+        va[db][2 * p + 1] = (s16x4_t){v8[4], v8[5], v8[6], v8[7]};
+      }
   };
   const int s0 = split * S * ATTN_CHUNK;
   const int sc_first = s0 + ATTN_CHUNK * wave;
@@ -456,7 +466,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int key = sc + 16 * kb + 4 * c + v;
+            const int key = sc + key_of(kb, 4 * c + v);
             const float x = key <= qpos[tt] ? st[kb][v] * scale : -INFINITY;
             st[kb][v] = x;
             mloc = fmaxf(mloc, x);
