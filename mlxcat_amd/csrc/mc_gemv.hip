@@ -1261,24 +1261,42 @@ int launch_rows_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, floa
   return MC_OK;
 }
 
-// One block.  Wave w routes tokens w, w + 4, ...: the E <= 256 bf16 logits (4 per lane),
-// softmax in fp32, TK rounds of the largest remaining probability (lowest expert on
-// ties), weights renormalised over the selection in selection order.  The selections stay
-// in LDS: thread e counts expert e's pairs, a scan over the experts gives the touched
-// list and the offsets, and thread e writes its pairs in ascending order.
+// One block of 16 waves.  Wave w routes tokens w, w + 16, ... (at most 4): the logits of
+// all its tokens are loaded first (one memory round trip), then per token the E <= 256 bf16
+// logits (4 per lane), softmax in fp32, TK rounds of the largest remaining probability
+// (lowest expert on ties), weights renormalised over the selection in selection order.
+// The selections stay in LDS: thread e counts expert e's pairs (16-byte LDS reads), a scan
+// over the experts gives the touched list and the offsets, and thread e writes its pairs
+// in ascending order.
 constexpr int MOE_ROUTE_PAIRS = 64 * 8;  // M <= 64 tokens x TK <= 8
+constexpr int MOE_ROUTE_WAVES = 16;
+constexpr int MOE_ROUTE_TPW = 64 / MOE_ROUTE_WAVES;  // tokens per wave, at most
+typedef int route_i4 __attribute__((ext_vector_type(4)));
 
-__global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, int M, int E, int TK, MoeRoute rt) {
-  __shared__ int s_sel[MOE_ROUTE_PAIRS];
+__global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const uint16_t* logits, int M, int E, int TK,
+                                                                         MoeRoute rt) {
+  __shared__ __align__(16) int s_sel[MOE_ROUTE_PAIRS];
   __shared__ int s_cnt[256], s_act[256];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int t = wave; t < M; t += 4) {
+  float lg[MOE_ROUTE_TPW][4];
+#pragma unroll
+  for (int u = 0; u < MOE_ROUTE_TPW; ++u) {
+    const int t = wave + MOE_ROUTE_WAVES * u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane + 64 * j;
+      lg[u][j] = t < M && ex < E ? bf16_to_f32(logits[(size_t)t * E + ex]) : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < MOE_ROUTE_TPW; ++u) {
+    const int t = wave + MOE_ROUTE_WAVES * u;
+    if (t >= M) break;  // uniform per wave
     float p[4];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int ex = lane + 64 * j;
-      p[j] = ex < E ? bf16_to_f32(logits[(size_t)t * E + ex]) : -INFINITY;
+      p[j] = lg[u][j];
       mx = fmaxf(mx, p[j]);
     }
 #pragma unroll
@@ -1322,31 +1340,47 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const uint16_t* logits, 
       rt.wts[t * TK + lane] = wmine / wsum;
     }
   }
+  const int P = M * TK, P4 = (P + 3) / 4;
+  if (tid < 4 * P4 - P) s_sel[P + tid] = -1;  // the last 16-byte group's padding
   __syncthreads();
-  const int P = M * TK;
-  for (int i = tid; i < P; i += 256) rt.sel[i] = s_sel[i];
+  for (int i = tid; i < P; i += 64 * MOE_ROUTE_WAVES) rt.sel[i] = s_sel[i];
+  const route_i4* sel4 = reinterpret_cast<const route_i4*>(s_sel);
   int n = 0;
-  if (tid < E)
-    for (int i = 0; i < P; ++i) n += s_sel[i] == tid;
-  s_cnt[tid] = n;
-  s_act[tid] = n > 0 ? 1 : 0;
+  if (tid < E) {
+#pragma unroll 8
+    for (int i = 0; i < P4; ++i) {
+      const route_i4 v = sel4[i];
+      n += (v.x == tid) + (v.y == tid) + (v.z == tid) + (v.w == tid);
+    }
+  }
+  if (tid < 256) {
+    s_cnt[tid] = n;
+    s_act[tid] = n > 0 ? 1 : 0;
+  }
   __syncthreads();
   // inclusive scans of the pair counts and of the touched flags (Hillis-Steele)
   for (int o = 1; o < 256; o <<= 1) {
-    const int c0 = tid >= o ? s_cnt[tid - o] : 0, a0 = tid >= o ? s_act[tid - o] : 0;
+    const int c0 = tid < 256 && tid >= o ? s_cnt[tid - o] : 0, a0 = tid < 256 && tid >= o ? s_act[tid - o] : 0;
     __syncthreads();
-    s_cnt[tid] += c0;
-    s_act[tid] += a0;
+    if (tid < 256) {
+      s_cnt[tid] += c0;
+      s_act[tid] += a0;
+    }
     __syncthreads();
   }
-  const int first = s_cnt[tid] - n;  // exclusive offset of expert tid's pairs
-  if (n > 0) {
+  if (tid < 256 && n > 0) {
+    const int first = s_cnt[tid] - n;  // exclusive offset of expert tid's pairs
     const int slot = s_act[tid] - 1;
     rt.act_e[slot] = tid;
     rt.off[slot] = first;
     int o = first;
-    for (int i = 0; i < P; ++i)
-      if (s_sel[i] == tid) rt.pairs[o++] = i;
+    for (int i = 0; i < P4; ++i) {
+      const route_i4 v = sel4[i];
+      if (v.x == tid) rt.pairs[o++] = 4 * i;
+      if (v.y == tid) rt.pairs[o++] = 4 * i + 1;
+      if (v.z == tid) rt.pairs[o++] = 4 * i + 2;
+      if (v.w == tid) rt.pairs[o++] = 4 * i + 3;
+    }
   }
   if (tid == 255) {
     rt.off[s_act[255]] = s_cnt[255];
@@ -1358,7 +1392,7 @@ int launch_moe_route(const uint16_t* logits, int M, int E, int TK, const MoeRout
   if (E < 1 || E > 256 || TK < 1 || TK > 8 || TK > E) return fail(MC_E_INVALID, "moe route: experts (<= 256) / top-k (<= 8)");
   if (M < 1) return MC_OK;
   if (M * TK > MOE_ROUTE_PAIRS) return fail(MC_E_INVALID, "moe route: more than 64 tokens");
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, st, logits, M, E, TK, rt);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(64 * MOE_ROUTE_WAVES), 0, st, logits, M, E, TK, rt);
   MC_HIP(hipGetLastError());
   return MC_OK;
 }
