@@ -1261,6 +1261,55 @@ int launch_rows_rmsnorm(const uint16_t* x, const uint16_t* w, int M, int H, floa
   return MC_OK;
 }
 
+// Wave-wide reductions for the routing block: DPP moves within rows of 16 lanes (swap
+// neighbours, swap pairs, mirror 8, mirror 16: every lane of a row then holds the row's
+// result), then the four rows' results read into scalar registers -- no LDS round trips.
+template <int CTRL>
+__device__ inline unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ inline float route_wave_max(float v) {
+  v = fmaxf(v, __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x141>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x140>(__float_as_uint(v))));
+  const unsigned u = __float_as_uint(v);
+  return fmaxf(fmaxf(__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 0)),
+                     __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 16))),
+               fmaxf(__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 32)),
+                     __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 48))));
+}
+__device__ inline float route_wave_sum(float v) {
+  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x140>(__float_as_uint(v)));
+  const unsigned u = __float_as_uint(v);
+  return (__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 0)) +
+          __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 16))) +
+         (__uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 32)) +
+          __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)u, 48)));
+}
+template <int CTRL>
+__device__ inline unsigned long long dpp_max_u64(unsigned long long k) {
+  const unsigned long long o = ((unsigned long long)dpp_u32<CTRL>((unsigned)(k >> 32)) << 32) | dpp_u32<CTRL>((unsigned)k);
+  return o > k ? o : k;
+}
+__device__ inline unsigned long long route_wave_max_u64(unsigned long long k) {
+  k = dpp_max_u64<0xB1>(k);
+  k = dpp_max_u64<0x4E>(k);
+  k = dpp_max_u64<0x141>(k);
+  k = dpp_max_u64<0x140>(k);
+  unsigned long long m = 0ull;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const unsigned long long x = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(unsigned)(k >> 32), 16 * r) << 32) |
+                                 (unsigned)__builtin_amdgcn_readlane((int)(unsigned)k, 16 * r);
+    m = x > m ? x : m;
+  }
+  return m;
+}
+
 // One block of 16 waves.  Wave w routes tokens w, w + 16, ... (at most 4): the logits of
 // all its tokens are loaded first (one memory round trip), then per token the E <= 256 bf16
 // logits (4 per lane), softmax in fp32, TK rounds of the largest remaining probability
@@ -1299,16 +1348,14 @@ __global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const u
       p[j] = lg[u][j];
       mx = fmaxf(mx, p[j]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = route_wave_max(mx);
     float den = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       p[j] = lane + 64 * j < E ? expf(p[j] - mx) : 0.f;
       den += p[j];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+    den = route_wave_sum(den);
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] /= den;
     unsigned taken = 0u;  // bit j: expert lane + 64 j already selected
@@ -1324,11 +1371,7 @@ __global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const u
           best = k > best ? k : best;
         }
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const unsigned long long ot = __shfl_xor(best, o);
-        best = ot > best ? ot : best;
-      }
+      best = route_wave_max_u64(best);
       const int ex = (int)(0xFFFFFFFFu - (unsigned)(best & 0xFFFFFFFFull));
       const float w = __uint_as_float((unsigned)(best >> 32));
       if ((ex & 63) == lane) taken |= 1u << (ex >> 6);
@@ -1358,19 +1401,43 @@ __global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const u
     s_act[tid] = n > 0 ? 1 : 0;
   }
   __syncthreads();
-  // inclusive scans of the pair counts and of the touched flags (Hillis-Steele)
-  for (int o = 1; o < 256; o <<= 1) {
-    const int c0 = tid < 256 && tid >= o ? s_cnt[tid - o] : 0, a0 = tid < 256 && tid >= o ? s_act[tid - o] : 0;
-    __syncthreads();
-    if (tid < 256) {
-      s_cnt[tid] += c0;
-      s_act[tid] += a0;
+  // exclusive offsets of the pair counts and of the touched experts: wave 0 scans the
+  // 256 entries, 4 consecutive per lane (lane sums, then a 6-step inclusive lane scan)
+  if (wave == 0) {
+    int c[4], a[4], cs = 0, as = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = s_cnt[4 * lane + j];
+      a[j] = s_act[4 * lane + j];
+      cs += c[j];
+      as += a[j];
     }
-    __syncthreads();
+    int ci = cs, ai = as;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int cu = __shfl_up(ci, o), au = __shfl_up(ai, o);
+      if (lane >= o) {
+        ci += cu;
+        ai += au;
+      }
+    }
+    int ce = ci - cs, ae = ai - as;  // exclusive prefix of this lane's first entry
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s_cnt[4 * lane + j] = ce;  // exclusive offsets now
+      s_act[4 * lane + j] = ae;
+      ce += c[j];
+      ae += a[j];
+    }
+    if (lane == 63) {
+      rt.off[ai] = ci;
+      *rt.n_active = ai;
+    }
   }
+  __syncthreads();
   if (tid < 256 && n > 0) {
-    const int first = s_cnt[tid] - n;  // exclusive offset of expert tid's pairs
-    const int slot = s_act[tid] - 1;
+    const int first = s_cnt[tid];  // exclusive offset of expert tid's pairs
+    const int slot = s_act[tid];
     rt.act_e[slot] = tid;
     rt.off[slot] = first;
     int o = first;
@@ -1381,10 +1448,6 @@ __global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const u
       if (v.z == tid) rt.pairs[o++] = 4 * i + 2;
       if (v.w == tid) rt.pairs[o++] = 4 * i + 3;
     }
-  }
-  if (tid == 255) {
-    rt.off[s_act[255]] = s_cnt[255];
-    *rt.n_active = s_act[255];
   }
 }
 

@@ -188,10 +188,12 @@ inline int emu_dpp(int src, int ctrl) {
   int s;
   if (ctrl < 0x100) s = (l & ~3) | ((ctrl >> (2 * (l & 3))) & 3);
   else if (ctrl == 0x141) s = (l & ~7) | (7 - (l & 7));
+  else if (ctrl == 0x140) s = (l & ~15) | (15 - (l & 15));
   else abort();
   return (int)emu::shfl_u((unsigned)src, s);
 }
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((src), (ctrl))
+#define __builtin_amdgcn_readlane(v, l) ((int)emu::shfl_u((unsigned)(v), (l)))
 inline int __any(int pred) { return emu::any(pred); }
 inline unsigned long long __ballot(int pred) { return emu::ballot(pred); }
 inline int __ffsll(long long x) { return __builtin_ffsll(x); }
