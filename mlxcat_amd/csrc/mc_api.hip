@@ -597,7 +597,7 @@ extern "C" int mc_batch_create(mc_model* m, int32_t max_rows, int32_t max_ctx, i
       const size_t E = (size_t)c.n_experts, P = (size_t)M * c.n_experts_per_tok;
       if ((rc = dev_zero(&b->moe_xn, (size_t)M * H)) || (rc = dev_zero(&b->moe_logits, (size_t)M * E)) ||
           (rc = dev_zero(&b->moe_act, P * c.moe_intermediate)) || (rc = dev_zero(&b->moe_out, P * H)) ||
-          (rc = dev_zero(&b->moe_i32, (size_t)c.n_layers + 2 * E + 1 + 2 * P)) || (rc = dev_zero(&b->moe_wts, P))) {
+          (rc = dev_zero(&b->moe_i32, (size_t)c.n_layers + 2 * E + 1 + 2 * P + 64 * E)) || (rc = dev_zero(&b->moe_wts, P))) {
         batch_free(b);
         return rc;
       }
@@ -794,12 +794,12 @@ static MoeRoute moe_route_of(mc_batch* b, int l) {
   rt.act_e = p; p += E;
   rt.off = p; p += E + 1;
   rt.pairs = p; p += P;
-  rt.sel = p;
+  rt.sel = p; p += P;
+  rt.slot_pairs = p;
   rt.wts = b->moe_wts;
   return rt;
 }
 
-// Blocks per touched expert: about 8 tiles each.
 // Blocks per touched expert: 4 of its 16-row tiles per block (one per wave).  Qwen3-30B-A3B
 // shape, 4 rows x 5 tokens, per step: 4 tiles 7.24 ms, 8 tiles 7.69, 2 tiles 7.71, 16 tiles 9.25.
 static int moe_blocks_per_expert(const QLinear& L) { return std::max(1, std::min(L.NT, (L.NT + 3) / 4)); }

@@ -1107,10 +1107,17 @@ __host__ __device__ constexpr size_t moe_lds_bytes(int GP) {
 template <int D>
 __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
   MC_DYN_LDS(smem);
+  __shared__ int s_pairs[64];
   const int slot = blockIdx.x / a.nb, jb = blockIdx.x - slot * a.nb;
-  if (slot >= *a.rt.n_active || jb >= a.NT) return;  // uniform over the block
-  const int e = a.rt.act_e[slot];
-  const int p0 = a.rt.off[slot], np = a.rt.off[slot + 1] - p0;
+  // the slot's routing, all in one round trip (slot < max_active <= E: every read is inside
+  // the arrays; a slot past the touched count returns below)
+  const int n_act = *a.rt.n_active, e = a.rt.act_e[slot];
+  const int p0 = a.rt.off[slot], p1 = a.rt.off[slot + 1];
+  const int my_pair = threadIdx.x < 64 ? a.rt.slot_pairs[(size_t)slot * 64 + threadIdx.x] : 0;
+  if (slot >= n_act || jb >= a.NT) return;  // uniform over the block
+  const int np = p1 - p0;
+  if (threadIdx.x < 64) s_pairs[threadIdx.x] = my_pair;
+  __syncthreads();
   const int GP = a.GP, XS = xrow_stride(GP), cpr = GP * 16, ng = 2 * GP;
   const int nkc = (GP + D - 1) / D;  // K-chunks per tile
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                            // [MOE_ROWS][XS]
@@ -1148,7 +1155,7 @@ __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
         cc[j] = i - mm[j] * cpr;
         v[j] = (u32x4){0u, 0u, 0u, 0u};
         if (in[j] && cc[j] * 8 < a.K) {
-          const int row = a.rt.pairs[p0 + q0 + mm[j]] / a.x_div;
+          const int row = s_pairs[q0 + mm[j]] / a.x_div;
           v[j] = *reinterpret_cast<const u32x4*>(a.x + (size_t)row * a.ldx + cc[j] * 8);
         }
       }
@@ -1187,7 +1194,7 @@ __global__ void __launch_bounds__(256) moe_gemv_kernel(MoeGemvArgs a) {
       for (int v = 0; v < 4; ++v) {
         const int m = 4 * c + v;
         const bool live = m < Mr;
-        const int pr = live ? a.rt.pairs[p0 + q0 + m] : 0;
+        const int pr = live ? s_pairs[q0 + m] : 0;
         if (a.epi == EPI_SWIGLU) {
           const float up = __shfl_xor(acc[0][v], 1);
           if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)pr * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[0][v]) * up);
@@ -1441,12 +1448,15 @@ __global__ void __launch_bounds__(64 * MOE_ROUTE_WAVES) moe_route_kernel(const u
     rt.act_e[slot] = tid;
     rt.off[slot] = first;
     int o = first;
+    int32_t* sp = rt.slot_pairs + (size_t)slot * 64;
     for (int i = 0; i < P4; ++i) {
       const route_i4 v = sel4[i];
-      if (v.x == tid) rt.pairs[o++] = 4 * i;
-      if (v.y == tid) rt.pairs[o++] = 4 * i + 1;
-      if (v.z == tid) rt.pairs[o++] = 4 * i + 2;
-      if (v.w == tid) rt.pairs[o++] = 4 * i + 3;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        if (v[h] == tid) {
+          sp[o - first] = 4 * i + h;
+          rt.pairs[o++] = 4 * i + h;
+        }
     }
   }
 }

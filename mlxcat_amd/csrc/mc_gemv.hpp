@@ -47,6 +47,7 @@ struct MoeRoute {
   int32_t* off = nullptr;       // [E + 1] offsets into pairs per touched expert
   int32_t* pairs = nullptr;     // [M * TK] pair numbers grouped by expert
   int32_t* sel = nullptr;       // [M * TK] selected expert of each pair
+  int32_t* slot_pairs = nullptr; // [E][64] pair numbers of touched slot s, ascending (M <= 64)
   float* wts = nullptr;         // [M * TK] renormalised routing weight of each pair
 };
 
