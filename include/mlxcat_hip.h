@@ -163,6 +163,12 @@ void mc_batch_destroy(mc_batch* b);
 int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt,
                     int32_t max_tokens, const mc_sampling* sp, int32_t* first_token,
                     int32_t* finished);
+/* mc_batch_insert after a prefix-cache hit (Scheduler.swift:960-990 prepareHitRow): the
+ * row's K/V already holds prompt positions [0, n_cached) (mc_batch_import_kv_block), and
+ * prefill resumes at n_cached (0 <= n_cached < n_prompt; MC_E_STATE unless the row's K/V
+ * length is n_cached). */
+int mc_batch_insert_cached(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt, int32_t n_cached,
+                           int32_t max_tokens, const mc_sampling* sp, int32_t* first_token, int32_t* finished);
 /* Admit a row whose first n_ctx-1 positions of K/V were filled by
  * mc_batch_fill_synthetic_kv; the last token of ctx is the pending current token. */
 int mc_batch_insert_prefilled(mc_batch* b, int32_t row, const int32_t* ctx, int32_t n_ctx,
@@ -187,6 +193,17 @@ int mc_batch_filter(mc_batch* b, const int32_t* rows, int32_t n);
  * on the same device, or the same batch); that row becomes inactive with this K/V and
  * length, ready for mc_batch_insert_prefilled.  MC_E_CAPACITY if the K/V does not fit. */
 int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int32_t dst_row);
+/* Prefix blocks (TrackA/BlockAwarePrefixCache.swift:140-162 payloadForBlock): positions
+ * [t0, t0 + n) of one row's K/V in the reference's per-layer cache-state layout, keys and
+ * values each [n_layers][n_kv][n][d] bf16 host arrays (layer l's state[0|1][0, :, t0..<t0+n, :],
+ * the tensors that TrackA/SafetensorsBlockIO.swift:40-50 writes as layer.l.keys / .values).
+ * t0 + n <= the row's K/V length. */
+int mc_batch_export_kv_block(mc_batch* b, int32_t row, int32_t t0, int32_t n, uint16_t* keys, uint16_t* values);
+/* The reverse (reconstructCache, TrackA/BlockAwarePrefixCache.swift:57-85, which concatenates
+ * a hit's blocks in order): writes positions [t0, t0 + n) of the row, t0 <= its K/V length;
+ * the row becomes inactive with K/V length t0 + n, ready for mc_batch_insert_cached. */
+int mc_batch_import_kv_block(mc_batch* b, int32_t row, int32_t t0, int32_t n, const uint16_t* keys,
+                             const uint16_t* values);
 int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len);
 /* Copy one row's K (which_v = 0) or V (1) of one layer to host: [n_kv][len][d] bf16. */
 int mc_batch_read_kv(mc_batch* b, int32_t layer, int32_t row, int32_t which_v, uint16_t* out);

@@ -28,6 +28,7 @@ EXPORTS = [
     "mc_batch_trim", "mc_batch_rollback", "mc_batch_kv_len", "mc_batch_read_kv", "mc_batch_read_attention",
     "mc_batch_read_logits",
     "mc_batch_history", "mc_batch_filter", "mc_batch_extract_kv", "mc_batch_read_router",
+    "mc_batch_insert_cached", "mc_batch_export_kv_block", "mc_batch_import_kv_block",
     "mc_forward", "mc_ngram_propose", "mc_accept", "mc_accept_noalloc", "mc_step", "mc_batch_stats", "mc_batch_call_widths",
     "mc_batch_set_profiling", "mc_batch_profile", "mc_probe_hbm_read",
 ]
@@ -97,6 +98,9 @@ def load(path: str = LIB_PATH):
         "mc_batch_destroy": (None, [P]),
         "mc_batch_insert": (C.c_int, [P, I32, P, I32, I32, P, P, P]),
         "mc_batch_insert_prefilled": (C.c_int, [P, I32, P, I32, I32, P]),
+        "mc_batch_insert_cached": (C.c_int, [P, I32, P, I32, I32, I32, P, P, P]),
+        "mc_batch_export_kv_block": (C.c_int, [P, I32, I32, I32, P, P]),
+        "mc_batch_import_kv_block": (C.c_int, [P, I32, I32, I32, P, P]),
         "mc_batch_fill_synthetic_kv": (C.c_int, [P, I32, I32, U64]),
         "mc_batch_remove": (C.c_int, [P, I32]),
         "mc_batch_trim": (C.c_int, [P, I32]),
@@ -261,6 +265,37 @@ class Batch:
         _check(load().mc_batch_insert(self.h, row, _p(p), len(p), max_tokens, C.byref(sampling), C.byref(tok),
                                       C.byref(fin)))
         return tok.value, fin.value
+
+    def insert_cached(self, row: int, prompt, n_cached: int, max_tokens: int, sampling: Sampling):
+        """insert() after a prefix hit: the row's K/V holds prompt[:n_cached] already
+        (import_kv_block) and prefill resumes at n_cached."""
+        p = _i32(prompt)
+        tok, fin = C.c_int32(), C.c_int32()
+        _check(load().mc_batch_insert_cached(self.h, row, _p(p), len(p), n_cached, max_tokens, C.byref(sampling),
+                                             C.byref(tok), C.byref(fin)))
+        return tok.value, fin.value
+
+    def export_kv_block(self, row: int, t0: int, n: int):
+        """Positions [t0, t0 + n) of the row's K/V as (keys, values), each
+        [n_layers][n_kv][n][d] uint16 (bf16 bits): the per-layer cache-state slices a prefix
+        block holds."""
+        c = self.model.cfg
+        keys = np.zeros((c.n_layers, c.n_kv_heads, n, c.head_dim), dtype=np.uint16)
+        values = np.zeros_like(keys)
+        _check(load().mc_batch_export_kv_block(self.h, row, t0, n, _p(keys), _p(values)))
+        return keys, values
+
+    def import_kv_block(self, row: int, t0: int, keys, values) -> None:
+        """Writes positions [t0, t0 + n) of the row from (keys, values) of export_kv_block's
+        shape; the row becomes inactive with K/V length t0 + n."""
+        c = self.model.cfg
+        k = np.ascontiguousarray(keys, dtype=np.uint16)
+        v = np.ascontiguousarray(values, dtype=np.uint16)
+        n = k.shape[2] if k.ndim == 4 else -1
+        want = (c.n_layers, c.n_kv_heads, n, c.head_dim)
+        if k.shape != want or v.shape != want:
+            raise ValueError(f"import_kv_block: keys / values must be {want}, got {k.shape} / {v.shape}")
+        _check(load().mc_batch_import_kv_block(self.h, row, t0, n, _p(k), _p(v)))
 
     def fill_synthetic_kv(self, row: int, n: int, seed: int) -> None:
         _check(load().mc_batch_fill_synthetic_kv(self.h, row, n, seed))

@@ -1074,23 +1074,29 @@ static int check_row(mc_batch* b, int row) {
   return MC_OK;
 }
 
-extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
-                               const mc_sampling* sp, int32_t* first_token, int32_t* finished) {
+// Admission with the first n_cached prompt positions' K/V already in the row (0: none).
+static int insert_row(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt, int32_t n_cached,
+                      int32_t max_tokens, const mc_sampling* sp, int32_t* first_token, int32_t* finished) {
   if (!b || !prompt || !sp || n_prompt < 1 || max_tokens < 1) return fail(MC_E_INVALID, "mc_batch_insert: bad argument");
   int rc = check_row(b, row);
   if (rc) return rc;
+  if (n_cached < 0 || n_cached >= n_prompt)
+    return fail(MC_E_INVALID, "mc_batch_insert: n_cached must lie in [0, n_prompt - 1]");
   if ((size_t)n_prompt + (size_t)max_tokens + (size_t)b->K1 + 1 > (size_t)b->cap)
     return fail(MC_E_CAPACITY, "mc_batch_insert: prompt + max_tokens exceeds the context capacity");
   MC_HIP(hipSetDevice(b->m->device));
   if ((rc = sync_kv_len(b))) return rc;
+  if (n_cached > 0 && (b->m->fake || b->kv_len_host[(size_t)row] != n_cached))
+    return fail(MC_E_STATE, "mc_batch_insert: the row's K/V length must equal n_cached");
   StepState& s = b->s;
   const int V = b->m->cfg.vocab;
   for (int i = 0; i < n_prompt; ++i)
     if (prompt[i] < 0 || prompt[i] >= V) return fail(MC_E_INVALID, "mc_batch_insert: token id out of range");
   if ((rc = set_row_i32(b, s.active, row, 0))) return rc;
-  b->kv_len_host[(size_t)row] = 0;
-  // prefill all but the last prompt token (Scheduler.swift:722-739), in chunks
-  int done = 0;
+  b->kv_len_host[(size_t)row] = n_cached;
+  // prefill all but the last prompt token (Scheduler.swift:722-739), in chunks; a prefix hit
+  // resumes at the matched count (Scheduler.swift:960-990, prefillRange matched ..< count)
+  int done = n_cached;
   while (done < n_prompt - 1) {
     const int cnt = std::min(PREFILL_CHUNK, n_prompt - 1 - done);
     int M;
@@ -1099,7 +1105,7 @@ extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, 
     b->kv_len_host[(size_t)row] += cnt;
     done += cnt;
   }
-  if (n_prompt > 1) b->widths.push_back(1);
+  if (n_prompt - 1 > n_cached) b->widths.push_back(1);
   // last prompt token with logits, then first-token sampling through the acceptance kernels
   {
     const int one = 1;
@@ -1126,6 +1132,17 @@ extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, 
   if (first_token) *first_token = res[0];
   if (finished) *finished = res[1];
   return MC_OK;
+}
+
+extern "C" int mc_batch_insert(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
+                               const mc_sampling* sp, int32_t* first_token, int32_t* finished) {
+  return insert_row(b, row, prompt, n_prompt, 0, max_tokens, sp, first_token, finished);
+}
+
+extern "C" int mc_batch_insert_cached(mc_batch* b, int32_t row, const int32_t* prompt, int32_t n_prompt,
+                                      int32_t n_cached, int32_t max_tokens, const mc_sampling* sp,
+                                      int32_t* first_token, int32_t* finished) {
+  return insert_row(b, row, prompt, n_prompt, n_cached, max_tokens, sp, first_token, finished);
 }
 
 extern "C" int mc_batch_fill_synthetic_kv(mc_batch* b, int32_t row, int32_t n, uint64_t seed) {
@@ -1238,6 +1255,10 @@ static std::vector<std::pair<int, int>> plan_row_moves(const int32_t* rows, int 
 
 // K/V positions [0, len) of one layer from (sk, sv) to (dk, dv): K blocks [n_kv][cap][d],
 // V blocks [n_kv][d][cap] with each side's own position stride.
+// Position stride of a batch's K/V cache: max_ctx rounded up to a 64-key sub-chunk (the
+// attention reads whole sub-chunks), not max_ctx itself.
+static int kv_stride(const mc_batch* b) { return b->kv.empty() ? b->cap : b->kv[0].cap; }
+
 static int copy_kv_block(uint16_t* dk, uint16_t* dv, int dcap, const uint16_t* sk, const uint16_t* sv, int scap,
                          int len, int nkv, int d, hipStream_t st) {
   if (len <= 0) return MC_OK;
@@ -1262,7 +1283,7 @@ extern "C" int mc_batch_filter(mc_batch* b, const int32_t* rows, int32_t n) {
   if (rc) return rc;
   const int R = b->R;
   const auto& c = b->m->cfg;
-  const int nkv = c.n_kv_heads, d = c.head_dim, V = b->s.V, cap = b->cap;
+  const int nkv = c.n_kv_heads, d = c.head_dim, V = b->s.V, cap = kv_stride(b);
   const size_t kv_row = (size_t)nkv * cap * d;  // elements of one row's K (and of its V) in one layer
   const bool kv = !b->m->fake;
   // K/V and generated-token counts: row blocks moved in place, through one spare block
@@ -1342,11 +1363,12 @@ extern "C" int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int3
   if (len > dst->cap) return fail(MC_E_CAPACITY, "extract_kv: the row's K/V exceeds the destination's capacity");
   if ((rc = set_row_i32(dst, dst->s.active, dst_row, 0))) return rc;
   if (!b->m->fake) {
-    const size_t skv = (size_t)c.n_kv_heads * b->cap * c.head_dim, dkv = (size_t)c.n_kv_heads * dst->cap * c.head_dim;
+    const int scap = kv_stride(b), dcap = kv_stride(dst);
+    const size_t skv = (size_t)c.n_kv_heads * scap * c.head_dim, dkv = (size_t)c.n_kv_heads * dcap * c.head_dim;
     for (int l = 0; l < c.n_layers; ++l) {
       const KVLayer &S = b->kv[(size_t)l], &D = dst->kv[(size_t)l];
-      if ((rc = copy_kv_block(D.k + (size_t)dst_row * dkv, D.v + (size_t)dst_row * dkv, dst->cap,
-                              S.k + (size_t)row * skv, S.v + (size_t)row * skv, b->cap, len, c.n_kv_heads,
+      if ((rc = copy_kv_block(D.k + (size_t)dst_row * dkv, D.v + (size_t)dst_row * dkv, dcap,
+                              S.k + (size_t)row * skv, S.v + (size_t)row * skv, scap, len, c.n_kv_heads,
                               c.head_dim, b->st)))
         return rc;
     }
@@ -1354,6 +1376,83 @@ extern "C" int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int3
   }
   dst->kv_len_host[(size_t)dst_row] = len;
   return set_row_i32(dst, dst->s.kv_len, dst_row, len);
+}
+
+// Prefix blocks (TrackA/BlockAwarePrefixCache.swift:140-162 payloadForBlock, :57-85
+// reconstructCache): positions [t0, t0 + n) of one row's K/V in the reference's per-layer
+// state layout, keys and values each [n_layers][n_kv][n][d] bf16 (layer l's slice
+// state[0 or 1][0, :, t0 ..< t0 + n, :]).  Both go through a device staging buffer in the
+// block layout, moved to or from the host by plain 1D copies (2D copies to pageable host
+// memory have returned partial rows on this runtime): K rows are contiguous in the cache
+// and move by device-side strided copies; V is stored [d][cap] per head and turns through a
+// device transpose.
+static int kv_block_io(mc_batch* b, int row, int t0, int n, uint16_t* keys, uint16_t* values, bool to_host) {
+  const auto& c = b->m->cfg;
+  const int nkv = c.n_kv_heads, d = c.head_dim, cap = kv_stride(b), L = c.n_layers;
+  const size_t per_layer = (size_t)nkv * n * d, kv_row = (size_t)nkv * cap * d, total = per_layer * L;
+  uint16_t* stage = nullptr;  // [2][L][nkv][n][d]: keys, then values
+  MC_HIP(hipMalloc((void**)&stage, total * 2 * 2));
+  int rc = MC_OK;
+  hipError_t e = hipSuccess;
+  if (!to_host) {
+    e = hipMemcpyAsync(stage, keys, total * 2, hipMemcpyHostToDevice, b->st);
+    if (e == hipSuccess) e = hipMemcpyAsync(stage + total, values, total * 2, hipMemcpyHostToDevice, b->st);
+  }
+  for (int l = 0; l < L && rc == MC_OK && e == hipSuccess; ++l) {
+    const KVLayer& kv = b->kv[(size_t)l];
+    uint16_t* krow = kv.k + (size_t)row * kv_row + (size_t)t0 * d;  // head h at + h cap d
+    uint16_t* vrow = kv.v + (size_t)row * kv_row;
+    uint16_t *sk = stage + per_layer * l, *sv = stage + total + per_layer * l;
+    if (to_host)
+      e = hipMemcpy2DAsync(sk, (size_t)n * d * 2, krow, (size_t)cap * d * 2, (size_t)n * d * 2, (size_t)nkv,
+                           hipMemcpyDeviceToDevice, b->st);
+    else
+      e = hipMemcpy2DAsync(krow, (size_t)cap * d * 2, sk, (size_t)n * d * 2, (size_t)n * d * 2, (size_t)nkv,
+                           hipMemcpyDeviceToDevice, b->st);
+    if (e == hipSuccess) rc = launch_kv_block_v(vrow, cap, sv, nkv, n, d, t0, to_host, b->st);
+  }
+  if (to_host && rc == MC_OK && e == hipSuccess) {
+    e = hipMemcpyAsync(keys, stage, total * 2, hipMemcpyDeviceToHost, b->st);
+    if (e == hipSuccess) e = hipMemcpyAsync(values, stage + total, total * 2, hipMemcpyDeviceToHost, b->st);
+  }
+  if (rc == MC_OK && e != hipSuccess) rc = fail(MC_E_HIP, hipGetErrorString(e));
+  const hipError_t es = hipStreamSynchronize(b->st);
+  const hipError_t ef = hipFree(stage);
+  if (rc == MC_OK && es != hipSuccess) rc = fail(MC_E_HIP, hipGetErrorString(es));
+  if (rc == MC_OK && ef != hipSuccess) rc = fail(MC_E_HIP, hipGetErrorString(ef));
+  return rc;
+}
+
+extern "C" int mc_batch_export_kv_block(mc_batch* b, int32_t row, int32_t t0, int32_t n, uint16_t* keys,
+                                        uint16_t* values) {
+  if (!b || !keys || !values) return fail(MC_E_INVALID, "export_kv_block: null argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if (b->m->fake) return fail(MC_E_STATE, "export_kv_block: fake model has no K/V");
+  if (t0 < 0 || n < 1) return fail(MC_E_INVALID, "export_kv_block: bad range");
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  if ((int64_t)t0 + n > b->kv_len_host[(size_t)row])
+    return fail(MC_E_INVALID, "export_kv_block: range past the row's K/V length");
+  return kv_block_io(b, row, t0, n, keys, values, true);
+}
+
+extern "C" int mc_batch_import_kv_block(mc_batch* b, int32_t row, int32_t t0, int32_t n, const uint16_t* keys,
+                                        const uint16_t* values) {
+  if (!b || !keys || !values) return fail(MC_E_INVALID, "import_kv_block: null argument");
+  int rc = check_row(b, row);
+  if (rc) return rc;
+  if (b->m->fake) return fail(MC_E_STATE, "import_kv_block: fake model has no K/V");
+  if (t0 < 0 || n < 1) return fail(MC_E_INVALID, "import_kv_block: bad range");
+  MC_HIP(hipSetDevice(b->m->device));
+  if ((rc = sync_kv_len(b))) return rc;
+  if (t0 > b->kv_len_host[(size_t)row])
+    return fail(MC_E_INVALID, "import_kv_block: t0 past the row's K/V length (blocks go in order)");
+  if ((int64_t)t0 + n > b->cap) return fail(MC_E_CAPACITY, "import_kv_block: block past the row's capacity");
+  if ((rc = set_row_i32(b, b->s.active, row, 0))) return rc;
+  if ((rc = kv_block_io(b, row, t0, n, const_cast<uint16_t*>(keys), const_cast<uint16_t*>(values), false))) return rc;
+  b->kv_len_host[(size_t)row] = t0 + n;
+  return set_row_i32(b, b->s.kv_len, row, t0 + n);
 }
 
 extern "C" int mc_batch_kv_len(mc_batch* b, int32_t row, int32_t* len) {

@@ -78,43 +78,18 @@ __device__ inline float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// q/k RMSNorm (Qwen3) + rotate-half RoPE of one head vector by one wave: lane < d/2 holds
-// the rotation pair (lane, lane + d/2).  The standalone kernel below and the fused attention
-// both use it, so a key (or query) has the same bits whichever path computes it.  Products
-// are not contracted into fused multiply-adds: every step rounds where it is written.
-// ---------------------------------------------------------------------------
-__device__ inline void rope_pair(const uint16_t* hp, const uint16_t* nw, const float* rope_cos, const float* rope_sin,
-                                 int d, int pos, float eps, int lane, uint16_t* o1, uint16_t* o2) {
-#pragma clang fp contract(off)
-  const int hd = d >> 1;
-  float x1 = 0.f, x2 = 0.f;
-  if (lane < hd) {
-    x1 = bf16_to_f32(hp[lane]);
-    x2 = bf16_to_f32(hp[lane + hd]);
-  }
-  if (nw) {
-    const float ss = wave_sum(x1 * x1 + x2 * x2);
-    const float r = 1.0f / sqrtf(ss / (float)d + eps);
-    if (lane < hd) {
-      x1 = bf16_to_f32(f32_to_bf16((x1 * r) * bf16_to_f32(nw[lane])));
-      x2 = bf16_to_f32(f32_to_bf16((x2 * r) * bf16_to_f32(nw[lane + hd])));
-    }
-  }
-  *o1 = *o2 = 0;
-  if (lane < hd) {
-    const float cs = rope_cos[(size_t)pos * hd + lane], sn = rope_sin[(size_t)pos * hd + lane];
-    *o1 = f32_to_bf16(x1 * cs - x2 * sn);
-    *o2 = f32_to_bf16(x1 * sn + x2 * cs);
-  }
-}
-
-// QB head vectors per wave at once (independent latency chains), each with rope_pair's
-// arithmetic, in two steps so that a caller can issue other loads in between: rope_load
-// issues the loads of vector i (hp[i] at position pos[i]; ok[i] false leaves it out) and
-// rope_finish normalises and rotates them.
+// QB head vectors per wave at once (independent latency chains) in two steps, so that a
+// caller can issue other loads in between: rope_load issues the loads of vector i (hp[i] at
+// position pos[i]) and rope_finish normalises and rotates them.  Every load is unconditional,
+// from an in-bounds address (lanes >= d/2 read lane 0's elements), and is selected afterwards:
+// a load under a lane or ok[i] condition becomes a branch with its own wait, and the QB
+// vectors would then load one round trip after another.  ok[i] false drops vector i; hp[i]
+// and pos[i] must still address a readable vector.
 template <int QB>
 struct RopeRegs {
-  float x1[QB], x2[QB], cs[QB], sn[QB], w1, w2;
+  uint16_t x1[QB], x2[QB], w1, w2;
+  float cs[QB], sn[QB];
+  bool v[QB];
 };
 
 template <int QB>
@@ -122,20 +97,17 @@ __device__ inline void rope_load(RopeRegs<QB>& g, const uint16_t* const (&hp)[QB
                                  const bool (&ok)[QB], const uint16_t* nw, const float* rope_cos,
                                  const float* rope_sin, int d, int lane) {
   const int hd = d >> 1;
-  g.w1 = g.w2 = 0.f;
-  if (nw && lane < hd) {
-    g.w1 = bf16_to_f32(nw[lane]);
-    g.w2 = bf16_to_f32(nw[lane + hd]);
-  }
+  const int l = lane < hd ? lane : 0;
+  const uint16_t* wp = nw ? nw : hp[0];  // without a norm the weights are read and not used
+  g.w1 = wp[l];
+  g.w2 = wp[l + hd];
 #pragma unroll
   for (int i = 0; i < QB; ++i) {
-    g.x1[i] = g.x2[i] = g.cs[i] = g.sn[i] = 0.f;
-    if (ok[i] && lane < hd) {
-      g.x1[i] = bf16_to_f32(hp[i][lane]);
-      g.x2[i] = bf16_to_f32(hp[i][lane + hd]);
-      g.cs[i] = rope_cos[(size_t)pos[i] * hd + lane];
-      g.sn[i] = rope_sin[(size_t)pos[i] * hd + lane];
-    }
+    g.v[i] = ok[i] && lane < hd;
+    g.x1[i] = hp[i][l];
+    g.x2[i] = hp[i][l + hd];
+    g.cs[i] = rope_cos[(size_t)pos[i] * hd + l];
+    g.sn[i] = rope_sin[(size_t)pos[i] * hd + l];
   }
 }
 
@@ -143,11 +115,20 @@ template <int QB>
 __device__ inline void rope_finish(RopeRegs<QB>& g, bool norm, int d, float eps, int lane, uint16_t (&o1)[QB],
                                    uint16_t (&o2)[QB]) {
 #pragma clang fp contract(off)
-  const int hd = d >> 1;
+  // the weights are taken here, with the vectors: otherwise their loads sink into the norm
+  // branch and start one round trip later
+  asm volatile("" ::"v"((uint32_t)g.w1), "v"((uint32_t)g.w2));
+  float x1[QB], x2[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i) {
+    x1[i] = g.v[i] ? bf16_to_f32(g.x1[i]) : 0.f;
+    x2[i] = g.v[i] ? bf16_to_f32(g.x2[i]) : 0.f;
+  }
   if (norm) {
+    const float w1 = bf16_to_f32(g.w1), w2 = bf16_to_f32(g.w2);
     float ss[QB];
 #pragma unroll
-    for (int i = 0; i < QB; ++i) ss[i] = g.x1[i] * g.x1[i] + g.x2[i] * g.x2[i];
+    for (int i = 0; i < QB; ++i) ss[i] = x1[i] * x1[i] + x2[i] * x2[i];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
@@ -155,17 +136,37 @@ __device__ inline void rope_finish(RopeRegs<QB>& g, bool norm, int d, float eps,
 #pragma unroll
     for (int i = 0; i < QB; ++i) {
       const float r = 1.0f / sqrtf(ss[i] / (float)d + eps);
-      if (lane < hd) {
-        g.x1[i] = bf16_to_f32(f32_to_bf16((g.x1[i] * r) * g.w1));
-        g.x2[i] = bf16_to_f32(f32_to_bf16((g.x2[i] * r) * g.w2));
+      if (g.v[i]) {
+        x1[i] = bf16_to_f32(f32_to_bf16((x1[i] * r) * w1));
+        x2[i] = bf16_to_f32(f32_to_bf16((x2[i] * r) * w2));
       }
     }
   }
 #pragma unroll
   for (int i = 0; i < QB; ++i) {
-    o1[i] = f32_to_bf16(g.x1[i] * g.cs[i] - g.x2[i] * g.sn[i]);
-    o2[i] = f32_to_bf16(g.x1[i] * g.sn[i] + g.x2[i] * g.cs[i]);
+    o1[i] = g.v[i] ? f32_to_bf16(x1[i] * g.cs[i] - x2[i] * g.sn[i]) : (uint16_t)0;
+    o2[i] = g.v[i] ? f32_to_bf16(x1[i] * g.sn[i] + x2[i] * g.cs[i]) : (uint16_t)0;
   }
+}
+
+// ---------------------------------------------------------------------------
+// q/k RMSNorm (Qwen3) + rotate-half RoPE of one head vector by one wave: lane < d/2 holds
+// the rotation pair (lane, lane + d/2).  The standalone kernel below and the fused attention
+// both go through rope_load / rope_finish, so a key (or query) has the same bits whichever
+// path computes it.  Products are not contracted into fused multiply-adds: every step rounds
+// where it is written.
+// ---------------------------------------------------------------------------
+__device__ inline void rope_pair(const uint16_t* hp, const uint16_t* nw, const float* rope_cos, const float* rope_sin,
+                                 int d, int pos, float eps, int lane, uint16_t* o1, uint16_t* o2) {
+  RopeRegs<1> g;
+  const uint16_t* const hps[1] = {hp};
+  const int ps[1] = {pos};
+  const bool ok[1] = {true};
+  rope_load<1>(g, hps, ps, ok, nw, rope_cos, rope_sin, d, lane);
+  uint16_t a[1], b[1];
+  rope_finish<1>(g, nw != nullptr, d, eps, lane, a, b);
+  *o1 = a[0];
+  *o2 = b[0];
 }
 
 // Grid (slot, head / 4), one wave per head: q heads to q_out, k heads and v heads appended
@@ -374,7 +375,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
 #pragma unroll
       for (int i = 0; i < KB; ++i)
 #pragma unroll
-        for (int e = 0; e < D / 64; ++e) vv[i][e] = ok[i] ? hk[i][(size_t)nkv * D + lane + 64 * e] : (uint16_t)0;
+        for (int e = 0; e < D / 64; ++e) vv[i][e] = hk[i][(size_t)nkv * D + lane + 64 * e];  // stored only if ok[i]
     }
     // loads of the prologue first (the queries of this wave, the new keys / values), then the
     // first sub-chunk of cached keys when it holds no key of this step
@@ -406,7 +407,7 @@ __global__ void __launch_bounds__(256) attn_flash_kernel(const uint16_t* q, KVLa
 #pragma unroll
         for (int i = 0; i < KB; ++i)
 #pragma unroll
-          for (int e = 0; e < D / 64; ++e) vv[i][e] = ok[i] ? hk[i][(size_t)nkv * D + lane + 64 * e] : (uint16_t)0;
+          for (int e = 0; e < D / 64; ++e) vv[i][e] = hk[i][(size_t)nkv * D + lane + 64 * e];  // stored only if ok[i]
       }
       uint16_t k1[KB], k2[KB];
       rope_finish<KB>(gk, f.k_norm != nullptr, D, f.eps, lane, k1, k2);
@@ -759,6 +760,42 @@ __global__ void kv_synth_kernel(KVLayer kv, int layer, int row, int nkv, int d, 
     if (wv) kv.v[(((size_t)row * nkv + h) * d + e) * kv.cap + p] = val;
     else kv.k[(((size_t)row * nkv + h) * kv.cap + p) * d + e] = val;
   }
+}
+
+// One 64 x 64 tile (64 positions x 64 channels) of one head's V between the cache's layout,
+// [d][cap] with the block at columns t0 .. t0 + n - 1, and a prefix block's [n][d]
+// (to_block: cache -> block).  Reads and writes are both along the fastest axis of their
+// array; the tile turns in LDS (row pitch 66 halves = 33 banks, so a column read is
+// conflict-free).
+__global__ void __launch_bounds__(256) kv_block_v_kernel(uint16_t* v, int cap, uint16_t* blk, int n, int d, int t0,
+                                                         int to_block) {
+  __shared__ uint16_t tile[64][66];
+  const int h = blockIdx.z, p0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  uint16_t* vh = v + (size_t)h * d * cap + t0;
+  uint16_t* bh = blk + (size_t)h * n * d;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if (to_block) {
+    for (int i = ty; i < 64; i += 4)  // tile[e - e0][p - p0]
+      if (e0 + i < d && p0 + tx < n) tile[i][tx] = vh[(size_t)(e0 + i) * cap + p0 + tx];
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4)
+      if (p0 + i < n && e0 + tx < d) bh[(size_t)(p0 + i) * d + e0 + tx] = tile[tx][i];
+  } else {
+    for (int i = ty; i < 64; i += 4)  // tile[p - p0][e - e0]
+      if (p0 + i < n && e0 + tx < d) tile[i][tx] = bh[(size_t)(p0 + i) * d + e0 + tx];
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4)
+      if (e0 + i < d && p0 + tx < n) vh[(size_t)(e0 + i) * cap + p0 + tx] = tile[tx][i];
+  }
+}
+
+int launch_kv_block_v(uint16_t* v_row, int cap, uint16_t* blk, int nkv, int n, int d, int t0, bool to_block,
+                      hipStream_t st) {
+  if (n <= 0) return MC_OK;
+  hipLaunchKernelGGL(kv_block_v_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)((d + 63) / 64), (unsigned)nkv),
+                     dim3(256), 0, st, v_row, cap, blk, n, d, t0, to_block ? 1 : 0);
+  MC_HIP(hipGetLastError());
+  return MC_OK;
 }
 
 int launch_kv_synth(KVLayer kv, int layer, int row, int nkv, int d, int n, uint64_t seed, hipStream_t st) {

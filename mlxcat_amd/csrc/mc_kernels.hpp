@@ -63,5 +63,9 @@ int launch_fake_logits(int arch, const int32_t* slot_tok, int M, int V, uint16_t
 
 // Fill positions [0, n) of a row with seeded synthetic bf16 K/V (matches the oracle).
 int launch_kv_synth(KVLayer kv, int layer, int row, int nkv, int d, int n, uint64_t seed, hipStream_t st);
+// Positions [t0, t0 + n) of one row's V (v_row: that row's [nkv][d][cap]) to or from a prefix
+// block's [nkv][n][d] (blk, device memory).
+int launch_kv_block_v(uint16_t* v_row, int cap, uint16_t* blk, int nkv, int n, int d, int t0, bool to_block,
+                      hipStream_t st);
 
 }  // namespace mc

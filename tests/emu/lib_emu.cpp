@@ -14,6 +14,7 @@
 //   case 8: mc_accept_noalloc against mc_accept, two calls
 //   case 9: the case-4 model, 4 rows: mc_batch_filter (a 3-cycle; a repeated row) and
 //           mc_batch_extract_kv + mc_batch_insert_prefilled against an unfiltered batch
+//   case 10: the case-4 model: prefix blocks exported, imported, and mc_batch_insert_cached
 // exit status 0 when everything matches.
 #include <cstdio>
 #include <cstdlib>
@@ -356,6 +357,95 @@ static int filter_case(mc_model* m, const mc_model_config& c) {
   return g_bad ? 1 : 0;
 }
 
+// case 10: prefix blocks: a row's K/V exported in the reference's block layout equals
+// mc_batch_read_kv; the blocks imported into another batch's row read back the same, and
+// mc_batch_insert_cached admits the row on top of them (the resumed prefill then has other
+// M than the full one, so the tokens after it are not compared here)
+static int prefix_case(mc_model* m, const mc_model_config& c) {
+  // capacities that are not multiples of 64 (the cache's position stride rounds them up)
+  const int K = 4, K1 = K + 1, V = c.vocab, B = 64, N = 150;
+  const int nkv = c.n_kv_heads, d = c.head_dim, L = c.n_layers;
+  mc_spec_config spec{1, K, 3, 8, 1, 0, 0};
+  std::vector<int32_t> p((size_t)N);
+  for (int i = 0; i < N; ++i) p[(size_t)i] = i >= 120 ? p[(size_t)i - 90] : (i * 29 + 7) % V;
+  mc_batch *a = nullptr, *b = nullptr;
+  check(mc_batch_create(m, 2, 250, K, &spec, &a), "batch_create");
+  check(mc_batch_create(m, 2, 190, K, &spec, &b), "batch_create");
+  mc_sampling sp{};
+  sp.reject_token = -1;
+  int32_t first_a = 0, first_b = 0, fin = 0;
+  check(mc_batch_insert(a, 0, p.data(), N, 30, &sp, &first_a, &fin), "insert");
+  check(mc_batch_insert(b, 0, p.data(), 40, 30, &sp, &first_b, &fin), "insert");
+  std::vector<std::vector<uint16_t>> full((size_t)2 * L);
+  for (int l = 0; l < L; ++l)
+    for (int wv = 0; wv < 2; ++wv) {
+      full[(size_t)2 * l + wv].resize((size_t)nkv * N * d);
+      check(mc_batch_read_kv(a, l, 0, wv, full[(size_t)2 * l + wv].data()), "read_kv");
+    }
+  const int ranges[3][2] = {{0, B}, {B, B}, {5, 37}};
+  for (const auto& rg : ranges) {
+    const int t0 = rg[0], n = rg[1];
+    std::vector<uint16_t> k((size_t)L * nkv * n * d), v(k.size());
+    check(mc_batch_export_kv_block(a, 0, t0, n, k.data(), v.data()), "export_kv_block");
+    size_t diff = 0;
+    for (int l = 0; l < L; ++l)
+      for (int h = 0; h < nkv; ++h)
+        for (int t = 0; t < n; ++t)
+          for (int e = 0; e < d; ++e) {
+            const size_t o = (((size_t)l * nkv + h) * n + t) * d + e, f = ((size_t)h * N + t0 + t) * d + e;
+            diff += k[o] != full[(size_t)2 * l][f];
+            diff += v[o] != full[(size_t)2 * l + 1][f];
+          }
+    printf("export [%d, %d): %zu elements differ\n", t0, t0 + n, diff);
+    if (diff) ++g_bad;
+    if (t0 % B == 0) check(mc_batch_import_kv_block(b, 1, t0, n, k.data(), v.data()), "import_kv_block");
+  }
+  int32_t len = 0;
+  check(mc_batch_kv_len(b, 1, &len), "kv_len");
+  size_t diff = 0;
+  for (int l = 0; l < L; ++l)
+    for (int wv = 0; wv < 2; ++wv) {
+      std::vector<uint16_t> x((size_t)nkv * len * d);
+      check(mc_batch_read_kv(b, l, 1, wv, x.data()), "read_kv");
+      for (int h = 0; h < nkv; ++h)
+        for (int t = 0; t < len; ++t)
+          for (int e = 0; e < d; ++e)
+            diff += x[((size_t)h * len + t) * d + e] != full[(size_t)2 * l + wv][((size_t)h * N + t) * d + e];
+    }
+  printf("imported row: %d positions, %zu elements differ\n", len, diff);
+  if (len != 2 * B || diff) ++g_bad;
+  if (mc_batch_insert_cached(b, 1, p.data(), N, 2 * B + 1, 30, &sp, &first_b, &fin) != MC_E_STATE) {
+    printf("insert_cached accepted a wrong n_cached\n");
+    ++g_bad;
+  }
+  check(mc_batch_insert_cached(b, 1, p.data(), N, 2 * B, 30, &sp, &first_b, &fin), "insert_cached");
+  check(mc_batch_kv_len(b, 1, &len), "kv_len");
+  printf("insert_cached: first token %d (full prefill %d), K/V length %d\n", first_b, first_a, len);
+  if (len != N) ++g_bad;
+  std::vector<int32_t> ot((size_t)2 * K1), cnt(2), f(2);
+  for (int st = 0; st < 2; ++st) check(mc_step(b, nullptr, nullptr, ot.data(), cnt.data(), f.data()), "step");
+  // extract and filter between these strides: the K/V must read back the same
+  mc_batch* e = nullptr;
+  check(mc_batch_create(m, 1, 170, K, &spec, &e), "batch_create");
+  check(mc_batch_extract_kv(a, 0, e, 0), "extract_kv");
+  if (!case9_same_kv(e, 0, a, 0, c)) { printf("extract across strides: K/V differs\n"); ++g_bad; }
+  const int32_t keep[2] = {1, 0};
+  check(mc_batch_filter(b, keep, 2), "filter");
+  mc_batch* a2 = nullptr;
+  check(mc_batch_create(m, 2, 250, K, &spec, &a2), "batch_create");
+  check(mc_batch_extract_kv(a, 0, a2, 1), "extract_kv");
+  check(mc_batch_filter(a2, keep, 2), "filter");
+  if (!case9_same_kv(a2, 0, a, 0, c)) { printf("filter: K/V differs\n"); ++g_bad; }
+  mc_batch_destroy(a2);
+  mc_batch_destroy(e);
+  mc_batch_destroy(a);
+  mc_batch_destroy(b);
+  printf("out-of-range buffer accesses: loads %lld stores %lld\n", emu::oob_loads, emu::oob_stores);
+  if (emu::oob_loads || emu::oob_stores) ++g_bad;
+  printf("%s\n", g_bad ? "FAIL" : "OK");
+  return g_bad ? 1 : 0;
+}
+
 int main(int argc, char** argv) {
   const int cs = argc > 1 ? atoi(argv[1]) : 0;
   emu::install_fault_handler();
@@ -371,7 +461,7 @@ int main(int argc, char** argv) {
   if (cs == 3) {  // 8 kv heads, GQA group 4
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
-  if (cs == 4 || cs == 9) {  // speculative steps: padding slots
+  if (cs == 4 || cs == 9 || cs == 10) {  // speculative steps: padding slots
     c.hidden = 512; c.n_q_heads = 32; c.n_kv_heads = 8; c.intermediate = 1024; c.vocab = 4096;
   }
   if (cs == 5) {  // Qwen3-MoE: 16 experts of width 128, top-4 (a 40-token prefill gives experts > 16 pairs)
@@ -383,6 +473,7 @@ int main(int argc, char** argv) {
   check(mc_model_create(&c, &m), "model_create");
   check(mc_model_init_synthetic(m, SEED), "init_synthetic");
   if (cs == 9) return filter_case(m, c);
+  if (cs == 10) return prefix_case(m, c);
   mc_spec_config spec{1, 5, 3, 8, 1, 0, 0};
   mc_batch* b = nullptr;
   check(mc_batch_create(m, 1, ctx, 5, &spec, &b), "batch_create");

@@ -108,3 +108,28 @@ def test_filter_and_extract_errors(hip, model):
     assert b.kv_len(0) > 32
     with pytest.raises(_lib.HipError):
         b.extract_kv(0, small, 0)  # more positions than the destination holds
+
+
+def test_filter_and_extract_at_unaligned_capacities(hip, model):
+    """Capacities that are not multiples of 64: the cache's position stride is the capacity
+    rounded up to a 64-key sub-chunk, and rows moved between batches of different strides
+    (250 -> 256, 190 -> 192, 170 -> 192) read back the same K/V and keep decoding the same."""
+    sc = spec(k=K, min_ctx=8, acceptance=1, single_row_only=0, greedy_only=0)
+    a = hip.Batch(model, 3, 250, sc)
+    for r in range(3):
+        a.insert(r, _prompt(r, TINY["vocab"]), 40, _sampling(hip, r))
+    _steps(a, 2)
+    e = hip.Batch(model, 1, 190, sc)
+    a.extract_kv(2, e, 0)
+    assert _same_kv(e, 0, a, 2)
+    f = hip.Batch(model, 2, 170, sc)
+    e.extract_kv(0, f, 1)
+    assert _same_kv(f, 1, a, 2)
+    b = hip.Batch(model, 3, 250, sc)
+    for r in range(3):
+        b.insert(r, _prompt(r, TINY["vocab"]), 40, _sampling(hip, r))
+    _steps(b, 2)
+    b.filter([2, 0])
+    assert _same_kv(b, 0, a, 2) and _same_kv(b, 1, a, 0)
+    want, got = _steps(a, 3), _steps(b, 3)
+    assert got[0] == want[2] and got[1] == want[0]
