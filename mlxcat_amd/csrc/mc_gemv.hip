@@ -155,46 +155,89 @@ __device__ inline void reduce_waves(f32x4 (&acc)[MT], const float* red, int lane
 }
 
 // The epilogue of one tile: lane holds tokens m = mt*16 + 4c + v of weight row n = 16t + r16.
+// Loads and cross-lane sums of the tile's tokens are issued all together (a token past M
+// reads row 0 and drops it): a load or a reduction under a per-token condition becomes a
+// branch with its own wait, and the tokens would take one round trip after another.
 template <int MT>
 __device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int c, int r16) {
   const int n = t * 16 + r16;
+  if (a.epi == EPI_SWIGLU) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int m = mt * 16 + 4 * c + v;
-      const bool live = m < a.M;
-      if (a.epi == EPI_SWIGLU) {
+      for (int v = 0; v < 4; ++v) {
+        const int m = mt * 16 + 4 * c + v;
         // rows interleave (gate_i, up_i): the even lane takes up_i from its odd neighbour
         const float up = __shfl_xor(acc[mt][v], 1);
-        if (live && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)m * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[mt][v]) * up);
-      } else if (a.epi == EPI_RESIDUAL) {
-        // residual add, and this tile's sum of squares of the new rows for the next RMSNorm
-        // (N % 16 == 0 here: the hidden size)
-        float q = 0.f;
-        if (live) {
-          uint16_t* yp = a.y + (size_t)m * a.ldy + n;
-          const uint16_t h = f32_to_bf16(acc[mt][v] + bf16_to_f32(*yp));
-          *yp = h;
-          const float rr = bf16_to_f32(h);
-          q = rr * rr;
-        }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
-        if (live && r16 == 0 && a.ss_out) a.ss_out[(size_t)m * a.ss_ld_out + t] = q;
-      } else {
-        const uint16_t h = f32_to_bf16(acc[mt][v]);
-        if (live && n < a.N) a.y[(size_t)m * a.ldy + n] = h;
-        if (a.amax) {
-          // tile argmax over 16 rows: 32-bit key (value key << 16 | 15 - row), lowest row on ties
-          unsigned key = (live && n < a.N) ? (bf16_order_key(h) << 16) | (unsigned)(15 - r16) : 0u;
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) key = max(key, (unsigned)__shfl_xor((int)key, o));
-          if (live && r16 == 0 && key)
-            a.amax[(size_t)m * a.NT + t] =
-                ((unsigned long long)(key >> 16) << 32) | (0xFFFFFFFFull - (unsigned)(t * 16 + 15 - (int)(key & 15u)));
-        }
+        if (m < a.M && !(r16 & 1) && n + 1 < a.N) a.y[(size_t)m * a.ldy + (n >> 1)] = f32_to_bf16(silu_f(acc[mt][v]) * up);
       }
+  } else if (a.epi == EPI_RESIDUAL) {
+    // residual add, and this tile's sum of squares of the new rows for the next RMSNorm
+    // (N % 16 == 0 here: the hidden size)
+    uint16_t old[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = mt * 16 + 4 * c + v;
+        old[mt][v] = a.y[(size_t)(m < a.M ? m : 0) * a.ldy + n];
+      }
+    float q[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = mt * 16 + 4 * c + v;
+        const uint16_t h = f32_to_bf16(acc[mt][v] + bf16_to_f32(old[mt][v]));
+        const float rr = bf16_to_f32(h);
+        q[mt][v] = m < a.M ? rr * rr : 0.f;
+        if (m < a.M) a.y[(size_t)m * a.ldy + n] = h;
+      }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) q[mt][v] += __shfl_xor(q[mt][v], o);
+    if (a.ss_out && r16 == 0)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = mt * 16 + 4 * c + v;
+          if (m < a.M) a.ss_out[(size_t)m * a.ss_ld_out + t] = q[mt][v];
+        }
+  } else {
+    unsigned key[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = mt * 16 + 4 * c + v;
+        const bool live = m < a.M && n < a.N;
+        const uint16_t h = f32_to_bf16(acc[mt][v]);
+        if (live) a.y[(size_t)m * a.ldy + n] = h;
+        // tile argmax over 16 rows: 32-bit key (value key << 16 | 15 - row), lowest row on ties
+        key[mt][v] = live ? (bf16_order_key(h) << 16) | (unsigned)(15 - r16) : 0u;
+      }
+    if (a.amax) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) key[mt][v] = max(key[mt][v], (unsigned)__shfl_xor((int)key[mt][v], o));
+      if (r16 == 0)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int m = mt * 16 + 4 * c + v;
+            const unsigned k = key[mt][v];
+            if (m < a.M && k)
+              a.amax[(size_t)m * a.NT + t] =
+                  ((unsigned long long)(k >> 16) << 32) | (0xFFFFFFFFull - (unsigned)(t * 16 + 15 - (int)(k & 15u)));
+          }
     }
   }
 }
@@ -377,16 +420,25 @@ __global__ void __launch_bounds__(256) qgemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       if (tid + 256 * q < cpr) *reinterpret_cast<u32x4*>(wl + (tid + 256 * q) * 8) = nw[q];
+    // the RW rows' butterflies interleaved, each in its fixed order (a branch between them
+    // would serialise their LDS round trips)
+    float q[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      float q = 0.f;
+      q[r] = 0.f;
 #pragma unroll
-      for (int v = 0; v < SL; ++v) q += ssv[r][v];
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
-      const int m = wave + GEMV_WAVES * r;
-      if (lane == 0 && m < Mr) rs[m] = 1.0f / sqrtf(q / (float)a.K + a.eps);
+      for (int v = 0; v < SL; ++v) q[r] += ssv[r][v];
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) q[r] += __shfl_xor(q[r], o);
+    if (lane == 0)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const int m = wave + GEMV_WAVES * r;
+        if (m < Mr) rs[m] = 1.0f / sqrtf(q[r] / (float)a.K + a.eps);
+      }
     lds_barrier();
   }
   // Staging in phases over SB chunks at a time (LDS reads, normalise, LDS stores, group sums,
@@ -578,14 +630,20 @@ __global__ void __launch_bounds__(MID_THREADS) qgemv_mid_kernel(GemvArgs a) {
   // ---- row scales of the fused RMSNorm, r[m] = 1 / sqrt(mean(x^2) + eps), fixed order ----
   if (a.norm_w) {
     if (tid < cpr) *reinterpret_cast<u32x4*>(wl + tid * 8) = nw;
+    // the eight rows' butterflies interleaved, each in its fixed order
+    float q[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float q = (ssq[j][0] + ssq[j][1]) + (ssq[j][2] + ssq[j][3]);
+    for (int j = 0; j < 8; ++j) q[j] = (ssq[j][0] + ssq[j][1]) + (ssq[j][2] + ssq[j][3]);
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
-      const int m = wave + MID_WAVES * j;
-      if (lane == 0 && m < Mr) rs[m] = 1.0f / sqrtf(q / (float)a.K + a.eps);
-    }
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] += __shfl_xor(q[j], o);
+    if (lane == 0)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int m = wave + MID_WAVES * j;
+        if (m < Mr) rs[m] = 1.0f / sqrtf(q[j] / (float)a.K + a.eps);
+      }
     lds_barrier();
   }
 
