@@ -158,8 +158,22 @@ __device__ inline void reduce_waves(f32x4 (&acc)[MT], const float* red, int lane
 // Loads and cross-lane sums of the tile's tokens are issued all together (a token past M
 // reads row 0 and drops it): a load or a reduction under a per-token condition becomes a
 // branch with its own wait, and the tokens would take one round trip after another.
+// The residual rows a tile's EPI_RESIDUAL epilogue adds to (row 0 for a token past M).
 template <int MT>
-__device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int c, int r16) {
+__device__ inline void load_residual(const GemvArgs& a, int t, int c, int r16, uint16_t (&old)[MT][4]) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = mt * 16 + 4 * c + v;
+      old[mt][v] = a.y[(size_t)(m < a.M ? m : 0) * a.ldy + t * 16 + r16];
+    }
+}
+
+// old: the tile's residual rows (load_residual) when EPI_RESIDUAL, else unused.
+template <int MT>
+__device__ inline void epilogue_with(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int c, int r16,
+                                     const uint16_t (&old)[MT][4]) {
   const int n = t * 16 + r16;
   if (a.epi == EPI_SWIGLU) {
 #pragma unroll
@@ -174,14 +188,6 @@ __device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t
   } else if (a.epi == EPI_RESIDUAL) {
     // residual add, and this tile's sum of squares of the new rows for the next RMSNorm
     // (N % 16 == 0 here: the hidden size)
-    uint16_t old[MT][4];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = mt * 16 + 4 * c + v;
-        old[mt][v] = a.y[(size_t)(m < a.M ? m : 0) * a.ldy + n];
-      }
     float q[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -242,6 +248,13 @@ __device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t
   }
 }
 
+template <int MT>
+__device__ inline void epilogue(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int c, int r16) {
+  uint16_t old[MT][4] = {};
+  if (a.epi == EPI_RESIDUAL) load_residual<MT>(a, t, c, r16, old);
+  epilogue_with<MT>(a, acc, t, c, r16, old);
+}
+
 // Device-coherent partial of unit (t, kr); no wait here (the arrival is counted later).
 template <int MT>
 __device__ inline void store_partial(const GemvArgs& a, const f32x4 (&acc)[MT], int t, int kr, int lane) {
@@ -261,6 +274,9 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // the residual rows go out with the first partials (one round trip for both)
+  uint16_t old[MT][4] = {};
+  if (a.epi == EPI_RESIDUAL) load_residual<MT>(a, t, c, r16, old);
   // the partials of KB K-ranges are loaded together (one memory round trip per KB ranges,
   // not per range: the tail of a launch is its last tile's reduction), then summed in
   // K-range order; ranges past the last are neither loaded nor summed
@@ -293,7 +309,7 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
     }
   }
   if (lane == 0) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  epilogue<MT>(a, acc, t, c, r16);
+  epilogue_with<MT>(a, acc, t, c, r16, old);
 }
 
 // Ordering of the split-K hand-over.  A K-range's partials are agent-scope (sc1) stores,
