@@ -108,36 +108,65 @@ __device__ inline void compute_unit(f32x4 (&acc)[MT], const WBuf<D>& w, const ui
                                     int Mr, int ngp, int wave, int c, int r16, uint32_t mask, uint32_t magic) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // per group pair: every LDS read of its groups and MT token tiles first, then all their
+  // MFMAs (independent chains back to back), then the scalings in the order of one
+  // element's sum (group 2j, then 2j + 1), so a tile's FMAs do not wait on its own fresh
+  // MFMA result while the other tiles' reads are still to go.  At MT = 4 (registers) one
+  // group and token tile at a time, in the same order.
+  constexpr int GB = MT >= 4 ? 1 : 2;
+  constexpr int TB = MT >= 4 ? 1 : MT;  // token tiles per batch
 #pragma unroll
   for (int i = 0; i < D; ++i) {
     const int j = wave + WS * i;
     if (j >= ngp) break;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      const bf16x8 wv0 = dequant_word(gi ? w.nib[i].z : w.nib[i].x, mask, magic);
-      const bf16x8 wv1 = dequant_word(gi ? w.nib[i].w : w.nib[i].y, mask, magic);
-      const uint32_t sbv = gi ? w.sb[i].y : w.sb[i].x;
-      const float sv = DQ_STEP * __uint_as_float(sbv << 16);
-      const float bv = __uint_as_float(sbv & 0xFFFF0000u) - sv;
-      const int kl = j * 128 + gi * 64;
-      const int gl = j * 2 + gi;
+    for (int g0 = 0; g0 < 2; g0 += GB)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        // token rows >= M read row Mr - 1: finite values whose results are never stored
-        const int m = min(mt * 16 + r16, Mr - 1);
-        const uint16_t* xrow = xl + m * XS + kl + 8 * c;
-        const bf16x8 xv0 = *reinterpret_cast<const bf16x8*>(xrow);
-        const bf16x8 xv1 = *reinterpret_cast<const bf16x8*>(xrow + 32);
-        f32x4 g = {0.f, 0.f, 0.f, 0.f};
-        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv0, wv0, g, 0, 0, 0);
-        g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv1, wv1, g, 0, 0, 0);
-        const f32x4 xs = *reinterpret_cast<const f32x4*>(xsum + gl * 16 * MT + mt * 16 + 4 * c);
+    for (int t0 = 0; t0 < MT; t0 += TB) {
+      bf16x8 xv[GB][TB][2];
+      f32x4 xs[GB][TB];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          acc[mt][v] = __builtin_fmaf(sv, g[v], acc[mt][v]);
-          acc[mt][v] = __builtin_fmaf(bv, xs[v], acc[mt][v]);
+      for (int b = 0; b < GB; ++b) {
+        const int gi = g0 + b;
+        const int kl = j * 128 + gi * 64;
+        const int gl = j * 2 + gi;
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          const int mt = t0 + tb;
+          // token rows >= M read row Mr - 1: finite values whose results are never stored
+          const int m = min(mt * 16 + r16, Mr - 1);
+          const uint16_t* xrow = xl + m * XS + kl + 8 * c;
+          xv[b][tb][0] = *reinterpret_cast<const bf16x8*>(xrow);
+          xv[b][tb][1] = *reinterpret_cast<const bf16x8*>(xrow + 32);
+          xs[b][tb] = *reinterpret_cast<const f32x4*>(xsum + gl * 16 * MT + mt * 16 + 4 * c);
         }
       }
+      f32x4 g[GB][TB];
+      float sv[GB], bv[GB];
+#pragma unroll
+      for (int b = 0; b < GB; ++b) {
+        const int gi = g0 + b;
+        const bf16x8 wv0 = dequant_word(gi ? w.nib[i].z : w.nib[i].x, mask, magic);
+        const bf16x8 wv1 = dequant_word(gi ? w.nib[i].w : w.nib[i].y, mask, magic);
+        const uint32_t sbv = gi ? w.sb[i].y : w.sb[i].x;
+        sv[b] = DQ_STEP * __uint_as_float(sbv << 16);
+        bv[b] = __uint_as_float(sbv & 0xFFFF0000u) - sv[b];
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+          g[b][tb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+          g[b][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[b][tb][0], wv0, g[b][tb], 0, 0, 0);
+          g[b][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[b][tb][1], wv1, g[b][tb], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < GB; ++b)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc[t0 + tb][v] = __builtin_fmaf(sv[b], g[b][tb][v], acc[t0 + tb][v]);
+            acc[t0 + tb][v] = __builtin_fmaf(bv[b], xs[b][tb][v], acc[t0 + tb][v]);
+          }
     }
   }
 }
@@ -274,9 +303,11 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  // the residual rows go out with the first partials (one round trip for both)
+  // the residual rows go out with the first partials (one round trip for both; at MT = 4
+  // after them, for registers)
   uint16_t old[MT][4] = {};
-  if (a.epi == EPI_RESIDUAL) load_residual<MT>(a, t, c, r16, old);
+  if constexpr (MT <= 3)
+    if (a.epi == EPI_RESIDUAL) load_residual<MT>(a, t, c, r16, old);
   // the partials of KB K-ranges are loaded together (one memory round trip per KB ranges,
   // not per range: the tail of a launch is its last tile's reduction), then summed in
   // K-range order; ranges past the last are neither loaded nor summed
@@ -309,6 +340,8 @@ __device__ inline void finish_tile(const GemvArgs& a, int t, int lane, int c, in
     }
   }
   if (lane == 0) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if constexpr (MT > 3)
+    if (a.epi == EPI_RESIDUAL) load_residual<MT>(a, t, c, r16, old);
   epilogue_with<MT>(a, acc, t, c, r16, old);
 }
 
