@@ -1382,10 +1382,9 @@ extern "C" int mc_batch_extract_kv(mc_batch* b, int32_t row, mc_batch* dst, int3
 // reconstructCache): positions [t0, t0 + n) of one row's K/V in the reference's per-layer
 // state layout, keys and values each [n_layers][n_kv][n][d] bf16 (layer l's slice
 // state[0 or 1][0, :, t0 ..< t0 + n, :]).  Both go through a device staging buffer in the
-// block layout, moved to or from the host by plain 1D copies (2D copies to pageable host
-// memory have returned partial rows on this runtime): K rows are contiguous in the cache
-// and move by device-side strided copies; V is stored [d][cap] per head and turns through a
-// device transpose.
+// block layout, moved to or from the host by one plain copy each: K rows are contiguous in
+// the cache and move by device-side strided copies; V is stored [d][cap] per head and
+// turns through a device transpose.
 static int kv_block_io(mc_batch* b, int row, int t0, int n, uint16_t* keys, uint16_t* values, bool to_host) {
   const auto& c = b->m->cfg;
   const int nkv = c.n_kv_heads, d = c.head_dim, cap = kv_stride(b), L = c.n_layers;
